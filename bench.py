@@ -1,0 +1,263 @@
+"""Benchmark: the SiLVANN attention hot path on one MI355X.
+
+`python bench.py [--gpus 1] [--steps K] [--warmup W]` prints ONE JSON line.
+
+Headline (`value`): config 2 of BASELINE.json — batched decode, 32 sequences with lengths U[1024, 32768]
+from the seed, 32 q / 4 kv heads, head_dim 128, fp16 K/V in 256-position pages under seeded permuted page
+tables — through the split-K decode door (silvann_gfx950_attention_decode_paged). A step is one decode of
+the whole batch; `value` is its algorithmic bytes (each cached K and V row once, plus q, o and the page
+table entries) × K over the wall time of the K steps, inputs resident in HBM.
+
+`roofline` is the dominant kernel's (decode_split): algorithmic bytes ÷ its average launch duration, timed
+live with hipEvents on the stream the library launches on, against 8 TB/s. `traffic` is the HBM bytes a
+launch moves per rocprofv3 FETCH_SIZE + WRITE_SIZE, read from profiles/traffic.json when it holds a
+measurement of this kernel and workload (else null).
+
+`secondary` holds the other configurations' lines (decode GB/s for C1 and C5; prefill TFLOP/s for C3 and
+C4 against 2.5 PFLOP/s dense fp16), each timed the same way.
+
+`cpu_baseline` is the reference's own x86_avx2 silicon family (oracle/_ref, built from the reference's
+sources) over the same batch, its doors called through its nn table on the host cores — both of the
+reference's decode routes (attention_scores + attention_mix; attention_weights + attention_residual_mix +
+attention_finish), the faster reported. Pages are gathered to the reference's contiguous layout first,
+outside the timing. Without oracle/_ref the C restatement (oracle/liboracle_attention.so, one core) is
+timed instead, as "port".
+"""
+from __future__ import annotations
+
+import argparse
+import ctypes as C
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+HBM_PEAK_GBS = 8000.0
+FP16_PEAK_TFLOPS = 2500.0
+METRIC = "decode-attn GB/s & % HBM peak; prefill-attn TFLOP/s & % MFMA peak"
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--no-secondary", action="store_true")
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--cpu-threads", type=int, default=int(os.environ.get("BENCH_CPU_THREADS", "16")))
+    ap.add_argument("--only", type=int, default=0, help="time only this config (1-5), no CPU leg")
+    return ap.parse_args()
+
+
+def prof_read(name):
+    import silvann_amd
+    L = silvann_amd.lib()
+    ms, n = C.c_double(0), C.c_uint64(0)
+    if L.silvann_gfx950_profile_read(name.encode(), C.byref(ms), C.byref(n)) != 0:
+        raise RuntimeError("profile read failed")
+    return ms.value, n.value
+
+
+def time_steps(step, steps, warmup, kernel):
+    """Warm up, then time exactly `steps` steps: wall clock between device synchronisations, and the named
+    kernel's hipEvent durations on the library's stream."""
+    import torch
+    import silvann_amd
+    L = silvann_amd.lib()
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    L.silvann_gfx950_profile_enable(1)
+    for k in ("decode_split", "decode_merge", "causal_mfma"):
+        prof_read(k)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        step()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    L.silvann_gfx950_profile_enable(0)
+    kms, n = prof_read(kernel)
+    others = {k: prof_read(k) for k in ("decode_split", "decode_merge", "causal_mfma") if k != kernel}
+    if silvann_amd.doors.launch_failed():
+        raise RuntimeError("a launch failed during the timed steps")
+    return wall, kms / max(n, 1), others
+
+
+def traffic_for(kernel, workload):
+    f = ROOT / "profiles" / "traffic.json"
+    if not f.exists():
+        return None
+    try:
+        d = json.loads(f.read_text())
+        return d.get(f"{kernel}:{workload}")
+    except Exception:
+        return None
+
+
+def decode_setup(w, dev):
+    import torch
+    from silvann_amd import verbs
+    t = lambda a: torch.from_numpy(a).to(dev)  # noqa: E731
+    lens = t(w.lens)
+    pages = None if w.pages is None else t(w.pages)
+    out = torch.zeros(w.rows * w.q_heads * w.head_dim, dtype=torch.float16, device=dev)
+    over = torch.zeros(1, dtype=torch.int32, device=dev)
+    need = verbs.decode_paged_scratch_bytes(w.q_heads, w.kv_heads, w.head_dim, w.most, w.rows)
+    scratch = torch.empty(max(need, 4), dtype=torch.uint8, device=dev)
+    from silvann_amd import doors
+
+    def step():
+        doors.attention_decode_paged(out, w.q, w.k, w.v, pages, w.pages_row, w.page_size, w.k_row, lens, w.q_heads,
+                                     w.kv_heads, w.head_dim, w.most, w.rows, scratch, over)
+    return step, out, over
+
+
+def causal_setup(w, dev):
+    import torch
+    from silvann_amd import doors
+    pages = None if w.pages is None else torch.from_numpy(w.pages).to(dev)
+    out = torch.zeros(w.rows * w.q_heads * w.head_dim, dtype=torch.float16, device=dev)
+    over = torch.zeros(1, dtype=torch.int32, device=dev)
+
+    def step():
+        doors.attention_causal_paged(out, w.q, w.k, w.v, pages, w.page_size, w.q_heads, w.kv_heads, w.head_dim,
+                                     w.first, w.rows, over)
+    return step, out, over
+
+
+def bench_decode(w, dev, steps, warmup):
+    step, out, over = decode_setup(w, dev)
+    wall, split_ms, others = time_steps(step, steps, warmup, "decode_split")
+    b = w.io_bytes()
+    merge_ms = others["decode_merge"][0] / max(others["decode_merge"][1], 1)
+    return {
+        "config": w.name, "unit": "GB/s", "value": b * steps / wall / 1e9, "ms_per_step": wall / steps * 1e3,
+        "bytes_per_step": b, "split_ms": split_ms, "merge_ms": merge_ms,
+        "kernel_gbs": b / (split_ms * 1e-3) / 1e9, "frac": b / (split_ms * 1e-3) / 1e9 / HBM_PEAK_GBS,
+    }, out
+
+
+def bench_causal(w, dev, steps, warmup):
+    step, out, over = causal_setup(w, dev)
+    wall, kms, _ = time_steps(step, steps, warmup, "causal_mfma")
+    f = w.flops()
+    return {
+        "config": w.name, "unit": "TFLOP/s", "value": f * steps / wall / 1e12, "ms_per_step": wall / steps * 1e3,
+        "flops_per_step": f, "kernel_ms": kms, "kernel_tflops": f / (kms * 1e-3) / 1e12,
+        "frac": f / (kms * 1e-3) / 1e12 / FP16_PEAK_TFLOPS,
+    }, out
+
+
+def cpu_baseline(w, threads):
+    """The reference x86_avx2 family over the whole C2 batch (both decode routes, the faster reported); the C
+    restatement on one core as "port" where oracle/_ref is absent."""
+    import numpy as np
+    from oracle.oracle import Oracle, RefFamily, ref_available
+    q = w.q.cpu().numpy() if hasattr(w.q, "cpu") else w.q
+    k = w.k.cpu().numpy() if hasattr(w.k, "cpu") else w.k
+    v = w.v.cpu().numpy() if hasattr(w.v, "cpu") else w.v
+    host = type(w)(**{**w.__dict__, "q": q, "k": k, "v": v})
+    rows = [host.gathered(u) for u in range(w.rows)]
+    qs = q.reshape(w.rows, -1)
+    if ref_available():
+        os.environ["SILVANN_CPU_THREADS"] = str(max(threads - 1, 0))
+        R = RefFamily()
+        routes = {"attention_scores+attention_mix": R.decode,
+                  "attention_weights+attention_residual_mix+attention_finish": R.decode_tiered}
+        kind, cores = "reference", threads
+    else:
+        O = Oracle()
+
+        def port(qq, kk, vv, qh, kvh, hd, n):
+            p = O.scores(qq, kk, qh, kvh, hd, n)
+            return O.mix(p, vv, qh, kvh, hd, n)
+        routes = {"oracle scores+mix": port}
+        kind, cores = "port", 1
+    best = None
+    budget = 20.0
+    for name, fn in routes.items():
+        reps, total, t_all = 0, 0.0, time.perf_counter()
+        while True:
+            for u in range(w.rows):
+                kk, vv = rows[u]
+                t0 = time.perf_counter()
+                fn(qs[u], kk, vv, w.q_heads, w.kv_heads, w.head_dim, int(w.lens[u]))
+                total += time.perf_counter() - t0
+            reps += 1
+            if time.perf_counter() - t_all > budget / len(routes) or reps >= 20:
+                break
+        gbs = w.io_bytes() * reps / total / 1e9
+        if best is None or gbs > best[0]:
+            best = (gbs, name, reps, total)
+    gbs, name, reps, total = best
+    return {"value": gbs, "unit": "GB/s", "cores": cores, "kind": kind,
+            "sample": f"full C2 batch ({w.rows} sequences, {int(w.lens.sum())} positions) x{reps}, route {name}, "
+                      f"{total:.1f} s of CPU work; pages gathered to contiguous outside the timing"}
+
+
+def main():
+    a = parse()
+    if a.gpus != 1:
+        print(f"bench.py: this build measures one GPU; --gpus {a.gpus} is not supported (every GPU box here has one "
+              "GPU, and the attention path's sharding across GPUs is described, not built)", file=sys.stderr)
+        sys.exit(2)
+    import torch
+    import silvann_amd
+    from silvann_amd import workloads as W
+    silvann_amd.lib()
+    dev = torch.device("cuda:0")
+
+    if a.only:
+        w = W.CONFIGS[a.only](dev=dev)
+        r = (bench_decode if a.only in (1, 2, 5) else bench_causal)(w, dev, a.steps, a.warmup)[0]
+        print(json.dumps(r), flush=True)
+        return
+
+    w2 = W.config2(dev=dev)
+    head, _ = bench_decode(w2, dev, a.steps, a.warmup)
+    secondary = []
+    if not a.no_secondary:
+        for n in (5, 1):
+            w = W.CONFIGS[n](dev=dev)
+            secondary.append(bench_decode(w, dev, max(5, a.steps // 2), a.warmup)[0])
+            del w
+        for n in (3, 4):
+            w = W.CONFIGS[n](dev=dev)
+            secondary.append(bench_causal(w, dev, max(3, a.steps // 4), min(a.warmup, 2))[0])
+            del w
+        torch.cuda.empty_cache()
+    cpu = None if a.no_cpu else cpu_baseline(w2, a.cpu_threads)
+
+    line = {
+        "metric": METRIC,
+        "value": round(head["value"], 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": a.steps,
+        "warmup": a.warmup,
+        "ms_per_step": round(head["ms_per_step"], 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f16 (fp32 accumulate)",
+        "data": "synthetic: seeded N(0,1) fp16 q/k/v, seeded lengths and permuted page tables",
+        "config": {"workload": w2.name, "sequences": w2.rows, "positions": int(w2.lens.sum()),
+                   "q_heads": w2.q_heads, "kv_heads": w2.kv_heads, "head_dim": w2.head_dim,
+                   "page_size": w2.page_size, "bytes_per_step": head["bytes_per_step"]},
+        "roofline": {"bound": "hbm", "achieved": round(head["kernel_gbs"], 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(head["frac"], 4), "traffic": traffic_for("decode_split", w2.name),
+                     "kernel": "decode_split", "kernel_ms": round(head["split_ms"], 5),
+                     "merge_ms": round(head["merge_ms"], 5)},
+        "secondary": [{k: (round(v, 5) if isinstance(v, float) else v) for k, v in s.items()} for s in secondary],
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

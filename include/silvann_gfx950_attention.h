@@ -1,0 +1,167 @@
+/* silvann_gfx950_attention.h — the C ABI of the MI355X (gfx950) attention library.
+ *
+ * Every entry point takes plain device pointers and sizes. All device pointers are addresses in the
+ * calling thread's current HIP device; every door is asynchronous on the library's stream for the calling
+ * thread (the legacy null stream unless `silvann_gfx950_set_stream` named another), returns once its kernels
+ * are queued, and allocates nothing the caller can see (the reference doors' rule).
+ *
+ * Layouts are the reference's:
+ *   q      [q_heads][head_dim] fp16 (decode), [rows][q_heads][head_dim] (causal)
+ *   k, v   [position][kv_heads][head_dim] fp16, query head h reading kv head h / (q_heads / kv_heads)
+ *   p      fp32 weights, a query head's row `length` long
+ *   res    fp32 residual a query head: [m, l, acc[head_dim]]  (head_dim + 2 floats)
+ *   over   the worker's fault word: a door whose fp16 answer overflows stores 0x4E504F56 ("NPOV") there
+ *
+ * The first block of doors has exactly the signature of a row of the reference's nn door table
+ * (engine/src/packages/nn/contracts/abi/gpu.cuh, `nn__CONTRACT__DOORS`); each comment cites the row
+ * and the generic body whose arithmetic it reproduces (engine/src/packages/nn/gpu/kernels/kernels.cuh).
+ * `SILVANN_GFX950_ROW_*` is that row's index in the table (a pointer slot after the table's uint32 size). */
+#ifndef SILVANN_GFX950_ATTENTION_H
+#define SILVANN_GFX950_ATTENTION_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ── rows of the reference's nn door table ─────────────────────────────────────────────────────── */
+
+/* gpu.cuh:119 attention_scores — kernels.cuh:1133-1141 (+ scores_head 894-915): p[h][t] = softmax_t(q_h·k_t / sqrt(hd)) */
+#define SILVANN_GFX950_ROW_ATTENTION_SCORES 25u
+void silvann_gfx950_attention_scores(float* p, const uint16_t* q, const uint16_t* k, uint64_t q_heads,
+                                     uint64_t kv_heads, uint64_t head_dim, uint64_t length);
+/* gpu.cuh:120 attention_mix — kernels.cuh:1156-1164 (+ mix_head 1144-1154): o[h][e] = fp16(Σ_t p[h][t] v_t[e]) */
+#define SILVANN_GFX950_ROW_ATTENTION_MIX 26u
+void silvann_gfx950_attention_mix(uint16_t* o, const float* p, const uint16_t* v, uint64_t q_heads,
+                                  uint64_t kv_heads, uint64_t head_dim, uint64_t length, unsigned int* over);
+/* gpu.cuh:122 attention_weights — kernels.cuh:1190-1221: p = e^(s - m) unnormalised, res[h] = {m, l} */
+#define SILVANN_GFX950_ROW_ATTENTION_WEIGHTS 28u
+void silvann_gfx950_attention_weights(float* p, float* res, const uint16_t* q, const uint16_t* k,
+                                      uint64_t q_heads, uint64_t kv_heads, uint64_t head_dim, uint64_t length);
+/* gpu.cuh:123 attention_residual_mix — kernels.cuh:1224-1238: res[h].acc[e] = Σ_t p[h][t] v_t[e] */
+#define SILVANN_GFX950_ROW_ATTENTION_RESIDUAL_MIX 29u
+void silvann_gfx950_attention_residual_mix(float* res, const float* p, const uint16_t* v, uint64_t q_heads,
+                                           uint64_t kv_heads, uint64_t head_dim, uint64_t length);
+/* gpu.cuh:124 attention_merge — kernels.cuh:1243-1255: two residuals into one; `into` may be `a` or `b` */
+#define SILVANN_GFX950_ROW_ATTENTION_MERGE 30u
+void silvann_gfx950_attention_merge(float* into, const float* a, const float* b, uint64_t q_heads,
+                                    uint64_t head_dim);
+/* gpu.cuh:125 attention_finish — kernels.cuh:1258-1267: o = fp16(acc / l) */
+#define SILVANN_GFX950_ROW_ATTENTION_FINISH 31u
+void silvann_gfx950_attention_finish(uint16_t* o, const float* res, uint64_t q_heads, uint64_t head_dim,
+                                     unsigned int* over);
+/* gpu.cuh:155 attention_causal_scores — kernels.cuh:2039-2049: row r (position first + r) over keys 0..first+r,
+ * weights at p + (r·q_heads + h)·(first + rows) */
+#define SILVANN_GFX950_ROW_ATTENTION_CAUSAL_SCORES 61u
+void silvann_gfx950_attention_causal_scores(float* p, const uint16_t* q, const uint16_t* k, uint64_t q_heads,
+                                            uint64_t kv_heads, uint64_t head_dim, uint64_t first, uint64_t rows);
+/* gpu.cuh:156 attention_causal_mix — kernels.cuh:2051-2060 */
+#define SILVANN_GFX950_ROW_ATTENTION_CAUSAL_MIX 62u
+void silvann_gfx950_attention_causal_mix(uint16_t* o, const float* p, const uint16_t* v, uint64_t q_heads,
+                                         uint64_t kv_heads, uint64_t head_dim, uint64_t first, uint64_t rows,
+                                         unsigned int* over);
+/* gpu.cuh:189 attention_scores_grouped — kernels.cuh:928-948: raw scaled scores, no softmax */
+#define SILVANN_GFX950_ROW_ATTENTION_SCORES_GROUPED 95u
+void silvann_gfx950_attention_scores_grouped(float* p, const uint16_t* q, const uint16_t* k, uint64_t q_heads,
+                                             uint64_t kv_heads, uint64_t head_dim, uint64_t length);
+/* gpu.cuh:190 attention_softmax_rows — kernels.cuh:1085-1100: each of `rows` rows (`length` apart) its softmax */
+#define SILVANN_GFX950_ROW_ATTENTION_SOFTMAX_ROWS 96u
+void silvann_gfx950_attention_softmax_rows(float* p, uint64_t rows, uint64_t length);
+/* gpu.cuh:191 attention_causal_scores_grouped — kernels.cuh:1028-1061: raw scaled causal scores */
+#define SILVANN_GFX950_ROW_ATTENTION_CAUSAL_SCORES_GROUPED 97u
+void silvann_gfx950_attention_causal_scores_grouped(float* p, const uint16_t* q, const uint16_t* k,
+                                                    uint64_t q_heads, uint64_t kv_heads, uint64_t head_dim,
+                                                    uint64_t first, uint64_t rows);
+/* gpu.cuh:192 attention_causal_softmax — kernels.cuh:1065-1081 */
+#define SILVANN_GFX950_ROW_ATTENTION_CAUSAL_SOFTMAX 98u
+void silvann_gfx950_attention_causal_softmax(float* p, uint64_t q_heads, uint64_t first, uint64_t rows);
+/* gpu.cuh:195 attention_weights_rows — doors.cuh:201-204,417-424 (attention_weights a row at a time) */
+#define SILVANN_GFX950_ROW_ATTENTION_WEIGHTS_ROWS 101u
+void silvann_gfx950_attention_weights_rows(float* p, float* res, const uint16_t* q, const uint16_t* k,
+                                           uint64_t q_heads, uint64_t kv_heads, uint64_t head_dim,
+                                           uint64_t first, uint64_t rows);
+/* gpu.cuh:196 attention_residual_mix_rows — doors.cuh:425-432 */
+#define SILVANN_GFX950_ROW_ATTENTION_RESIDUAL_MIX_ROWS 102u
+void silvann_gfx950_attention_residual_mix_rows(float* res, const float* p, const uint16_t* v, uint64_t q_heads,
+                                                uint64_t kv_heads, uint64_t head_dim, uint64_t first,
+                                                uint64_t rows);
+/* gpu.cuh:222 attention_scores_grouped_rows — kernels.cuh:953-972: row u's lens[u] keys at k + u·k_row */
+#define SILVANN_GFX950_ROW_ATTENTION_SCORES_GROUPED_ROWS 128u
+void silvann_gfx950_attention_scores_grouped_rows(float* p, uint64_t p_row, const uint16_t* q, uint64_t q_row,
+                                                  const uint16_t* k, uint64_t k_row, const uint32_t* lens,
+                                                  uint64_t q_heads, uint64_t kv_heads, uint64_t head_dim,
+                                                  uint64_t most, uint64_t rows);
+/* gpu.cuh:223 attention_softmax_lens — kernels.cuh:1104-1110 */
+#define SILVANN_GFX950_ROW_ATTENTION_SOFTMAX_LENS 129u
+void silvann_gfx950_attention_softmax_lens(float* p, uint64_t p_row, const uint32_t* lens, uint64_t heads,
+                                           uint64_t rows);
+/* gpu.cuh:224 attention_mix_rows — kernels.cuh:1169-1178 */
+#define SILVANN_GFX950_ROW_ATTENTION_MIX_ROWS 130u
+void silvann_gfx950_attention_mix_rows(uint16_t* o, uint64_t o_row, const float* p, uint64_t p_row,
+                                       const uint16_t* v, uint64_t v_row, const uint32_t* lens, uint64_t q_heads,
+                                       uint64_t kv_heads, uint64_t head_dim, uint64_t rows, unsigned int* over);
+
+/* The nn door table's row count at ABI version 9 (gpu.cuh:93-230): new rows are appended after it. */
+#define SILVANN_GFX950_NN_ROWS 137u
+
+/* ── rows appended after the reference's table (gpu.cuh:86-88: rows are only ever appended) ──────────
+ * The reference has no paged cache (its KV is one contiguous `[position][kv_head][head_dim]` plane a layer).
+ * These rows take a cache pool of pages, each `page_size` positions × kv_heads × head_dim fp16 (K and V in
+ * pools of their own), and a page table: logical page `j` of row `u` is physical page `pages[u·pages_row + j]`.
+ * `pages` NULL means the cache is contiguous, as the reference's (then `k`/`v` for row u start at
+ * `u·k_row` halves; `page_size` and `pages_row` are ignored). Their answers are the reference's attention over
+ * the gathered-contiguous cache (decode: `attention_scores` + `attention_mix`; causal: `causal_scores` +
+ * `causal_mix`). */
+
+/* One query position a row over its own cache: row u's q_heads at q + u·q_heads·head_dim attend positions
+ * 0 .. lens[u]-1; out o + u·q_heads·head_dim. Split-K flash decoding: `scratch` holds the partial residuals,
+ * `silvann_gfx950_attention_decode_paged_scratch` bytes (0 if it needs none). `most` is the largest lens[u]
+ * (a bound the grid is sized by; lens[u] <= most is the caller's promise). A row with lens[u] == 0 answers 0.
+ * Split-K form of the reference's decode verb (engine/src/packages/nn/cpu/opcodes/attention__abi.cuh:129-160),
+ * many rows as `attention_scores_grouped_rows` (gpu.cuh:222) takes them. */
+#define SILVANN_GFX950_ROW_ATTENTION_DECODE_PAGED 137u
+void silvann_gfx950_attention_decode_paged(uint16_t* o, const uint16_t* q, const uint16_t* k, const uint16_t* v,
+                                           const uint32_t* pages, uint64_t pages_row, uint64_t page_size,
+                                           uint64_t k_row, const uint32_t* lens, uint64_t q_heads,
+                                           uint64_t kv_heads, uint64_t head_dim, uint64_t most, uint64_t rows,
+                                           float* scratch, unsigned int* over);
+uint64_t silvann_gfx950_attention_decode_paged_scratch(uint64_t q_heads, uint64_t kv_heads, uint64_t head_dim,
+                                                       uint64_t most, uint64_t rows);
+
+/* Causal prefill of `rows` new positions first .. first+rows-1 over the cache, which already holds their
+ * keys and values and the `first` before them: row r's q_heads at q + r·q_heads·head_dim attend positions
+ * 0 .. first + r; out o + r·q_heads·head_dim. One sequence (page table `pages`, `pages` NULL for a contiguous
+ * cache). The fused form of `attention_causal_scores_grouped` + `attention_causal_softmax` +
+ * `attention_causal_mix` (gpu.cuh:191,192,156) as the reference's `nn__attention__rows` runs them
+ * (attention__abi.cuh:407-414), on fp16 MFMA with fp32 accumulation; no weights are materialised. */
+#define SILVANN_GFX950_ROW_ATTENTION_CAUSAL_PAGED 138u
+void silvann_gfx950_attention_causal_paged(uint16_t* o, const uint16_t* q, const uint16_t* k, const uint16_t* v,
+                                           const uint32_t* pages, uint64_t page_size, uint64_t q_heads,
+                                           uint64_t kv_heads, uint64_t head_dim, uint64_t first, uint64_t rows,
+                                           unsigned int* over);
+
+/* ── library control (no reference counterpart: the reference family's launch and sys doors do this) ── */
+
+/* The stream the calling thread's doors are queued on (a hipStream_t; NULL is the legacy null stream, the
+ * reference family's choice, amd_rocm_base/nn.cuh:25-34). Thread-local, as a runner thread is a worker's. */
+void silvann_gfx950_set_stream(void* stream);
+void* silvann_gfx950_get_stream(void);
+/* Nonzero if a launch on this thread failed since the last call (the reference remembers a refused launch so
+ * that the next compute_completed answers false, amd_rocm_base/nn.cuh:29-33); clears it. */
+int silvann_gfx950_launch_failed(void);
+/* Live kernel timing: with profiling on, this thread's doors bracket their main kernels with hipEvents on
+ * their stream. `kernel` is "decode_split", "decode_merge" or "causal_mfma"; read synchronises, answers the
+ * summed milliseconds and the launch count since the last read, and clears them. Answers -1 for an unknown
+ * name or a failed event. */
+void silvann_gfx950_profile_enable(int on);
+int silvann_gfx950_profile_read(const char* kernel, double* total_ms, uint64_t* launches);
+/* The library's build: "gfx950 <kernels> <version>". */
+const char* silvann_gfx950_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* SILVANN_GFX950_ATTENTION_H */

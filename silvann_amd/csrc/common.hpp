@@ -1,0 +1,75 @@
+// common.hpp — what every kernel file of the gfx950 attention library shares: the fp16 vector types the
+// MFMA builtins take, the fault word, the wave-level folds, and the launch bookkeeping (stream and the
+// remembered launch failure).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#define SILVANN_EXPORT extern "C" __attribute__((visibility("default")))
+
+namespace silvann {
+
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+// The fault a door stores when an fp16 answer overflows: "NPOV" (reference
+// packages/nn/contracts/objects/primitives.cuh:57, kernels.cuh:29-40).
+constexpr unsigned int kFaultOverflow = 0x4E504F56u;
+constexpr float kLog2e = 1.4426950408889634f;
+
+// fp32 -> fp16 with round-to-nearest-even, subnormals kept: the hardware conversion gives the bits of the
+// reference's hand-written one (kernels.cuh:2763-2808) for every finite input. A finite input whose answer
+// is infinite overflowed — past 65504 or carried there by the rounding — and is flagged; an input that was
+// already inf or NaN passes through unflagged, as the reference does.
+__device__ __forceinline__ uint16_t to_half(float f, bool& hit) {
+    _Float16 h = (_Float16)f;
+    uint16_t b = __builtin_bit_cast(uint16_t, h);
+    if ((b & 0x7FFFu) == 0x7C00u && __builtin_isfinite(f)) hit = true;
+    return b;
+}
+
+__device__ __forceinline__ float half_bits_to_float(uint16_t b) {
+    return (float)__builtin_bit_cast(_Float16, b);
+}
+
+// e^x as 2^(x·log2 e) on the transcendental unit; -inf gives 0.
+__device__ __forceinline__ float fast_exp(float x) { return __builtin_amdgcn_exp2f(x * kLog2e); }
+
+// Folds over the whole wave (64 lanes) and over the four 16-lane groups of a lane's column.
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+    for (int s = 32; s >= 1; s >>= 1) v = fmaxf(v, __shfl_xor(v, s));
+    return v;
+}
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+    for (int s = 32; s >= 1; s >>= 1) v += __shfl_xor(v, s);
+    return v;
+}
+// Over lanes l, l^16, l^32, l^48: the four row-groups of an MFMA 16x16 tile's column.
+__device__ __forceinline__ float groups_max(float v) {
+    v = fmaxf(v, __shfl_xor(v, 16));
+    return fmaxf(v, __shfl_xor(v, 32));
+}
+__device__ __forceinline__ float groups_sum(float v) {
+    v += __shfl_xor(v, 16);
+    return v + __shfl_xor(v, 32);
+}
+
+// ── launch bookkeeping ─────────────────────────────────────────────────────────────────────────────
+hipStream_t stream();
+// Records a failed launch (printed once, remembered until silvann_gfx950_launch_failed reads it).
+void check_launch(const char* what);
+// Live kernel timing for the benchmark: when enabled on this thread, a door brackets its named kernel
+// with hipEvents on its stream; silvann_gfx950_profile_read sums them.
+void prof_begin(int kernel);
+void prof_end(int kernel);
+enum ProfKernel : int { kProfDecodeSplit = 0, kProfDecodeMerge = 1, kProfCausal = 2, kProfKernels = 3 };
+// Records a door that refused its operands without launching (printed, remembered the same way).
+void refuse(const char* what);
+
+}  // namespace silvann

@@ -1,0 +1,497 @@
+// doors.hip — the reference's nn attention door rows, each with its exact signature, on gfx950.
+//
+// The reference splits attention into doors that hand fp32 weights `p` between them (scores → mix,
+// weights → residual_mix, causal scores → softmax → mix). Every door here keeps that contract bit-for-bit in
+// layout: what it writes into `p` and `res` is where and what the reference's body writes
+// (kernels.cuh:885-1267, 2036-2060; doors.cuh:414-432), within fp32 rounding. Four kernels serve all 17 rows,
+// each told the row geometry of its door:
+//   scores_raw    a workgroup per (row, kv head, 16-head block, 256 keys); a thread per key computes the
+//                 dots of all the block's query heads (held in LDS) with its key: the key is read once for the
+//                 group (kernels.cuh:917-948's point), and the scaled scores go to `p`
+//   softmax_rows  a workgroup per weight row: its max, e^(x - max), their sum; normalised, or left
+//                 unnormalised with {m, l} into the residual (the weights doors)
+//   mix_rows      a workgroup per (row, kv head, 64 dims): 4 waves split the keys, a lane a dim, every query
+//                 head of the group accumulated from one read of each value; the waves meet in LDS
+//   merge/finish  a thread per head / per element.
+// The fused decode and causal rows (decode.hip, prefill.hip) are the fast paths; these doors are the
+// reference's contract for callers that read `p` or `res` themselves.
+#include <math.h>
+#include <stdio.h>
+
+#include "common.hpp"
+#include "../../include/silvann_gfx950_attention.h"
+
+namespace silvann {
+namespace {
+
+// How a door's rows lie in its operands.
+enum Mode : int {
+    kSingle = 0,       // one query (scores, mix, weights, residual_mix): length, p[h·length + t]
+    kCausal = 1,       // rows r at first + r (causal_*): len first+r+1, q row r·qh·hd, p (r·qh+h)·span, k/v shared
+    kLens = 2,         // rows u with their own keys (*_rows of NN-115): len lens[u], q u·q_row, k/v u·k_row,
+                       //   p u·p_row + h·len, o u·o_row
+    kByRow = 3,        // the one-row door a row at a time (weights_rows, residual_mix_rows, doors.cuh:417-432):
+                       //   len first+r+1, q row r·qh·hd, p r·qh·span + h·len, res (r·qh+h)·(hd+2)
+};
+
+struct Geom {
+    int mode;
+    uint64_t length, first, span;
+    uint64_t q_row, k_row, p_row, o_row;
+    const uint32_t* lens;
+    uint32_t q_heads, kv_heads, head_dim;
+};
+
+struct RowAt {
+    uint64_t len, q, k, p, hstride, o;
+};
+
+template <int MODE>
+__device__ __forceinline__ RowAt row_at(const Geom& G, uint64_t u) {
+    RowAt r;
+    const uint64_t qh = G.q_heads, hd = G.head_dim;
+    if constexpr (MODE == kCausal) {
+        r.len = G.first + u + 1; r.q = u * qh * hd; r.k = 0; r.p = u * qh * G.span; r.hstride = G.span;
+        r.o = u * qh * hd;
+    } else if constexpr (MODE == kLens) {
+        r.len = G.lens[u]; r.q = u * G.q_row; r.k = u * G.k_row; r.p = u * G.p_row; r.hstride = r.len;
+        r.o = u * G.o_row;
+    } else if constexpr (MODE == kByRow) {
+        r.len = G.first + u + 1; r.q = u * qh * hd; r.k = 0; r.p = u * qh * G.span; r.hstride = r.len;
+        r.o = u * qh * (hd + 2);
+    } else {
+        static_assert(MODE == kSingle, "row geometry");
+        r.len = G.length; r.q = 0; r.k = 0; r.p = 0; r.hstride = G.length; r.o = 0;
+    }
+    return r;
+}
+
+constexpr int kHB = 16;   // query heads a block of scores_raw / mix_rows holds
+
+// Scaled dots of a block of query heads with 256 keys; the query heads' rows in LDS as floats.
+template <int MODE>
+__global__ __launch_bounds__(256) void scores_raw(float* p, const uint16_t* q, const uint16_t* k, Geom G,
+                                                  uint32_t hblocks, uint32_t nheads, float scale) {
+    extern __shared__ float qs[];   // [nheads][head_dim]
+    const uint64_t u = blockIdx.z;
+    const uint32_t g = blockIdx.y / hblocks, hb = blockIdx.y % hblocks;
+    const uint32_t group = G.q_heads / G.kv_heads, hd = G.head_dim;
+    const uint32_t h0 = g * group + hb * nheads;
+    const int nh = (int)min(nheads, group - hb * nheads);
+    const RowAt R = row_at<MODE>(G, u);
+    const uint64_t t = (uint64_t)blockIdx.x * 256 + threadIdx.x;
+    if ((uint64_t)blockIdx.x * 256 >= R.len) return;
+    for (uint32_t i = threadIdx.x; i < (uint32_t)nh * hd; i += 256)
+        qs[i] = half_bits_to_float(q[R.q + (uint64_t)(h0 + i / hd) * hd + i % hd]);
+    __syncthreads();
+    if (t >= R.len) return;
+    const uint64_t row = (uint64_t)G.kv_heads * hd;
+    const uint16_t* kr = k + R.k + t * row + (uint64_t)g * hd;
+    float dot[kHB];
+#pragma unroll
+    for (int j = 0; j < kHB; ++j) dot[j] = 0.0f;
+    if ((hd & 1u) == 0 && (((uintptr_t)kr) & 3u) == 0) {
+        const uint32_t* k2 = (const uint32_t*)kr;
+        for (uint32_t e = 0; e < hd / 2; ++e) {
+            const uint32_t pair = k2[e];
+            const float k0 = half_bits_to_float((uint16_t)(pair & 0xFFFFu));
+            const float k1 = half_bits_to_float((uint16_t)(pair >> 16));
+#pragma unroll
+            for (int j = 0; j < kHB; ++j)
+                if (j < nh) dot[j] += qs[j * hd + 2 * e] * k0 + qs[j * hd + 2 * e + 1] * k1;
+        }
+    } else {
+        for (uint32_t e = 0; e < hd; ++e) {
+            const float kv = half_bits_to_float(kr[e]);
+#pragma unroll
+            for (int j = 0; j < kHB; ++j)
+                if (j < nh) dot[j] += qs[j * hd + e] * kv;
+        }
+    }
+#pragma unroll
+    for (int j = 0; j < kHB; ++j)
+        if (j < nh) p[R.p + (uint64_t)(h0 + j) * R.hstride + t] = dot[j] * scale;
+}
+
+// A weight row's softmax in place. `res` non-null: unnormalised e^(x - m), {m, l} into res (the weights
+// doors); else normalised by 1 / l (kernels.cuh:1085-1094).
+template <int MODE>
+__global__ __launch_bounds__(256) void softmax_rows(float* p, float* res, Geom G, uint64_t nrows) {
+    __shared__ float red[8];
+    const uint64_t i = blockIdx.x + (uint64_t)blockIdx.y * gridDim.x;
+    if (i >= nrows) return;
+    uint64_t len, off, roff = 0;
+    const uint64_t qh = G.q_heads;
+    if constexpr (MODE == kCausal) {
+        len = G.first + i / qh + 1; off = i * G.span;
+    } else if constexpr (MODE == kLens) {
+        const uint64_t u = i / qh, h = i % qh;
+        len = G.lens[u]; off = u * G.p_row + h * len;
+    } else if constexpr (MODE == kByRow) {
+        const uint64_t r = i / qh, h = i % qh;
+        len = G.first + r + 1; off = r * qh * G.span + h * len; roff = i * (G.head_dim + 2ull);
+    } else {
+        static_assert(MODE == kSingle, "row geometry");
+        len = G.length; off = i * G.length; roff = i * (G.head_dim + 2ull);
+    }
+    float* ph = p + off;
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    float mx = -INFINITY;
+    for (uint64_t t = threadIdx.x; t < len; t += 256) mx = fmaxf(mx, ph[t]);
+    mx = wave_max(mx);
+    if (lane == 0) red[w] = mx;
+    __syncthreads();
+    const float top = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    float part = 0.0f;
+    for (uint64_t t = threadIdx.x; t < len; t += 256) {
+        const float e = expf(ph[t] - top);
+        ph[t] = e;
+        part += e;
+    }
+    part = wave_sum(part);
+    if (lane == 0) red[4 + w] = part;
+    __syncthreads();
+    const float sum = red[4] + red[5] + red[6] + red[7];
+    if (res) {
+        if (threadIdx.x == 0) {
+            res[roff] = top;
+            res[roff + 1] = sum;
+        }
+        return;
+    }
+    const float inv = 1.0f / sum;
+    for (uint64_t t = threadIdx.x; t < len; t += 256) ph[t] *= inv;
+}
+
+// o[h][d] = Σ_t p[h][t] v_t[d] for a block of query heads of one kv head and 64 dims; into fp16 `o` (with
+// the overflow flag) or, `acc_out` set, into the fp32 residual's acc.
+template <int MODE>
+__global__ __launch_bounds__(256) void mix_rows(uint16_t* o, float* acc_out, const float* p, const uint16_t* v,
+                                                Geom G, uint32_t hblocks, uint32_t dblocks, unsigned int* over) {
+    __shared__ float part[4][kHB][64];
+    const uint64_t u = blockIdx.z;
+    const uint32_t g = blockIdx.y / hblocks, hb = blockIdx.y % hblocks;
+    const uint32_t group = G.q_heads / G.kv_heads, hd = G.head_dim;
+    const uint32_t h0 = g * group + hb * kHB;
+    const int nh = (int)min((uint32_t)kHB, group - hb * kHB);
+    const uint32_t d = (blockIdx.x % dblocks) * 64 + (threadIdx.x & 63);
+    const int w = threadIdx.x >> 6;
+    const RowAt R = row_at<MODE>(G, u);
+    const uint64_t row = (uint64_t)G.kv_heads * hd;
+    float acc[kHB];
+#pragma unroll
+    for (int j = 0; j < kHB; ++j) acc[j] = 0.0f;
+    if (d < hd) {
+        const uint16_t* vc = v + R.k + (uint64_t)g * hd + d;
+        const float* pb = p + R.p + (uint64_t)h0 * R.hstride;
+        for (uint64_t t = w; t < R.len; t += 4) {
+            const float vv = half_bits_to_float(vc[t * row]);
+#pragma unroll
+            for (int j = 0; j < kHB; ++j)
+                if (j < nh) acc[j] += pb[(uint64_t)j * R.hstride + t] * vv;
+        }
+    }
+#pragma unroll
+    for (int j = 0; j < kHB; ++j) part[w][j][threadIdx.x & 63] = acc[j];
+    __syncthreads();
+    if (w != 0 || d >= hd) return;
+    bool hit = false;
+    for (int j = 0; j < nh; ++j) {
+        const float s = part[0][j][threadIdx.x] + part[1][j][threadIdx.x] + part[2][j][threadIdx.x] +
+                        part[3][j][threadIdx.x];
+        if (acc_out) {
+            acc_out[R.o + (uint64_t)(h0 + j) * (hd + 2) + 2 + d] = s;
+        } else {
+            o[R.o + (uint64_t)(h0 + j) * hd + d] = to_half(s, hit);
+        }
+    }
+    if (hit) *over = kFaultOverflow;
+}
+
+// kernels.cuh:1243-1255: a thread a head; a head's m and l are read before anything of it is written.
+__global__ void merge_heads(float* into, const float* a, const float* b, uint64_t q_heads, uint64_t head_dim) {
+    const uint64_t h = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (h >= q_heads) return;
+    const uint64_t w = head_dim + 2;
+    const float ma = a[h * w], la = a[h * w + 1], mb = b[h * w], lb = b[h * w + 1];
+    const float m = fmaxf(ma, mb);
+    const float fa = expf(ma - m), fb = expf(mb - m);
+    for (uint64_t e = 0; e < head_dim; ++e) into[h * w + 2 + e] = a[h * w + 2 + e] * fa + b[h * w + 2 + e] * fb;
+    into[h * w] = m;
+    into[h * w + 1] = la * fa + lb * fb;
+}
+
+// kernels.cuh:1258-1267
+__global__ void finish_heads(uint16_t* o, const float* res, uint64_t q_heads, uint64_t head_dim, unsigned int* over) {
+    const uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= q_heads * head_dim) return;
+    const uint64_t h = i / head_dim, w = head_dim + 2;
+    bool hit = false;
+    o[i] = to_half(res[h * w + 2 + i % head_dim] / res[h * w + 1], hit);
+    if (hit) *over = kFaultOverflow;
+}
+
+Geom geom(int mode, uint64_t q_heads, uint64_t kv_heads, uint64_t head_dim) {
+    Geom G = {};
+    G.mode = mode;
+    G.q_heads = (uint32_t)q_heads;
+    G.kv_heads = (uint32_t)kv_heads;
+    G.head_dim = (uint32_t)head_dim;
+    return G;
+}
+
+bool heads_ok(const char* door, uint64_t q_heads, uint64_t kv_heads, uint64_t head_dim, uint64_t rows) {
+    if (kv_heads == 0 || q_heads == 0 || head_dim == 0 || q_heads % kv_heads != 0 || head_dim > 8192 ||
+        q_heads > 65535 || rows > 65535) {
+        refuse(door);
+        return false;
+    }
+    return true;
+}
+
+uint32_t dims_for(uint32_t head_dim) {
+    // query heads a scores_raw block holds: 16, fewer where 16 rows of head_dim floats would pass 64 KB
+    uint32_t n = kHB;
+    while (n > 1 && (uint64_t)n * head_dim * 4 > 65536) n >>= 1;
+    return n;
+}
+
+void launch_scores(float* p, const uint16_t* q, const uint16_t* k, const Geom& G, uint64_t rows, uint64_t most) {
+    if (rows == 0 || most == 0) return;
+    const uint32_t group = G.q_heads / G.kv_heads;
+    const uint32_t nheads = dims_for(G.head_dim);
+    const uint32_t hblocks = (group + nheads - 1) / nheads;
+    const dim3 grid((uint32_t)((most + 255) / 256), G.kv_heads * hblocks, (uint32_t)rows);
+    const float scale = 1.0f / sqrtf((float)G.head_dim);
+    const size_t lds = nheads * G.head_dim * sizeof(float);
+    hipStream_t st = stream();
+    switch (G.mode) {
+        case kCausal: scores_raw<kCausal><<<grid, 256, lds, st>>>(p, q, k, G, hblocks, nheads, scale); break;
+        case kLens: scores_raw<kLens><<<grid, 256, lds, st>>>(p, q, k, G, hblocks, nheads, scale); break;
+        case kByRow: scores_raw<kByRow><<<grid, 256, lds, st>>>(p, q, k, G, hblocks, nheads, scale); break;
+        default: scores_raw<kSingle><<<grid, 256, lds, st>>>(p, q, k, G, hblocks, nheads, scale); break;
+    }
+}
+
+void launch_softmax(float* p, float* res, const Geom& G, uint64_t nrows) {
+    if (nrows == 0) return;
+    const uint32_t x = (uint32_t)(nrows < 65535 ? nrows : 65535);
+    const dim3 grid(x, (uint32_t)((nrows + x - 1) / x));
+    hipStream_t st = stream();
+    switch (G.mode) {
+        case kCausal: softmax_rows<kCausal><<<grid, 256, 0, st>>>(p, res, G, nrows); break;
+        case kLens: softmax_rows<kLens><<<grid, 256, 0, st>>>(p, res, G, nrows); break;
+        case kByRow: softmax_rows<kByRow><<<grid, 256, 0, st>>>(p, res, G, nrows); break;
+        default: softmax_rows<kSingle><<<grid, 256, 0, st>>>(p, res, G, nrows); break;
+    }
+}
+
+void launch_mix(uint16_t* o, float* acc_out, const float* p, const uint16_t* v, const Geom& G, uint64_t rows,
+                unsigned int* over) {
+    if (rows == 0) return;
+    const uint32_t group = G.q_heads / G.kv_heads;
+    const uint32_t hblocks = (group + kHB - 1) / kHB;
+    const uint32_t dblocks = (G.head_dim + 63) / 64;
+    const dim3 grid(dblocks, G.kv_heads * hblocks, (uint32_t)rows);
+    hipStream_t st = stream();
+    switch (G.mode) {
+        case kCausal: mix_rows<kCausal><<<grid, 256, 0, st>>>(o, acc_out, p, v, G, hblocks, dblocks, over); break;
+        case kLens: mix_rows<kLens><<<grid, 256, 0, st>>>(o, acc_out, p, v, G, hblocks, dblocks, over); break;
+        case kByRow: mix_rows<kByRow><<<grid, 256, 0, st>>>(o, acc_out, p, v, G, hblocks, dblocks, over); break;
+        default: mix_rows<kSingle><<<grid, 256, 0, st>>>(o, acc_out, p, v, G, hblocks, dblocks, over); break;
+    }
+}
+
+}  // namespace
+}  // namespace silvann
+
+using namespace silvann;
+
+// gpu.cuh:119 — kernels.cuh:1133-1141
+SILVANN_EXPORT void silvann_gfx950_attention_scores(float* p, const uint16_t* q, const uint16_t* k, uint64_t q_heads,
+                                                    uint64_t kv_heads, uint64_t head_dim, uint64_t length) {
+    if (!heads_ok("attention_scores", q_heads, kv_heads, head_dim, 1)) return;
+    Geom G = geom(kSingle, q_heads, kv_heads, head_dim);
+    G.length = length;
+    launch_scores(p, q, k, G, 1, length);
+    launch_softmax(p, nullptr, G, q_heads);
+    check_launch("attention_scores");
+}
+
+// gpu.cuh:120 — kernels.cuh:1156-1164
+SILVANN_EXPORT void silvann_gfx950_attention_mix(uint16_t* o, const float* p, const uint16_t* v, uint64_t q_heads,
+                                                 uint64_t kv_heads, uint64_t head_dim, uint64_t length,
+                                                 unsigned int* over) {
+    if (!heads_ok("attention_mix", q_heads, kv_heads, head_dim, 1)) return;
+    Geom G = geom(kSingle, q_heads, kv_heads, head_dim);
+    G.length = length;
+    launch_mix(o, nullptr, p, v, G, 1, over);
+    check_launch("attention_mix");
+}
+
+// gpu.cuh:122 — kernels.cuh:1190-1221
+SILVANN_EXPORT void silvann_gfx950_attention_weights(float* p, float* res, const uint16_t* q, const uint16_t* k,
+                                                     uint64_t q_heads, uint64_t kv_heads, uint64_t head_dim,
+                                                     uint64_t length) {
+    if (!heads_ok("attention_weights", q_heads, kv_heads, head_dim, 1)) return;
+    Geom G = geom(kSingle, q_heads, kv_heads, head_dim);
+    G.length = length;
+    launch_scores(p, q, k, G, 1, length);
+    launch_softmax(p, res, G, q_heads);
+    check_launch("attention_weights");
+}
+
+// gpu.cuh:123 — kernels.cuh:1224-1238
+SILVANN_EXPORT void silvann_gfx950_attention_residual_mix(float* res, const float* p, const uint16_t* v,
+                                                          uint64_t q_heads, uint64_t kv_heads, uint64_t head_dim,
+                                                          uint64_t length) {
+    if (!heads_ok("attention_residual_mix", q_heads, kv_heads, head_dim, 1)) return;
+    Geom G = geom(kSingle, q_heads, kv_heads, head_dim);
+    G.length = length;
+    launch_mix(nullptr, res, p, v, G, 1, nullptr);
+    check_launch("attention_residual_mix");
+}
+
+// gpu.cuh:124 — kernels.cuh:1243-1255
+SILVANN_EXPORT void silvann_gfx950_attention_merge(float* into, const float* a, const float* b, uint64_t q_heads,
+                                                   uint64_t head_dim) {
+    if (q_heads == 0) return;
+    merge_heads<<<(uint32_t)((q_heads + 63) / 64), 64, 0, stream()>>>(into, a, b, q_heads, head_dim);
+    check_launch("attention_merge");
+}
+
+// gpu.cuh:125 — kernels.cuh:1258-1267
+SILVANN_EXPORT void silvann_gfx950_attention_finish(uint16_t* o, const float* res, uint64_t q_heads,
+                                                    uint64_t head_dim, unsigned int* over) {
+    const uint64_t n = q_heads * head_dim;
+    if (n == 0) return;
+    finish_heads<<<(uint32_t)((n + 255) / 256), 256, 0, stream()>>>(o, res, q_heads, head_dim, over);
+    check_launch("attention_finish");
+}
+
+// gpu.cuh:155 — kernels.cuh:2039-2049
+SILVANN_EXPORT void silvann_gfx950_attention_causal_scores(float* p, const uint16_t* q, const uint16_t* k,
+                                                           uint64_t q_heads, uint64_t kv_heads, uint64_t head_dim,
+                                                           uint64_t first, uint64_t rows) {
+    if (!heads_ok("attention_causal_scores", q_heads, kv_heads, head_dim, rows)) return;
+    Geom G = geom(kCausal, q_heads, kv_heads, head_dim);
+    G.first = first;
+    G.span = first + rows;
+    launch_scores(p, q, k, G, rows, first + rows);
+    launch_softmax(p, nullptr, G, rows * q_heads);
+    check_launch("attention_causal_scores");
+}
+
+// gpu.cuh:156 — kernels.cuh:2051-2060
+SILVANN_EXPORT void silvann_gfx950_attention_causal_mix(uint16_t* o, const float* p, const uint16_t* v,
+                                                        uint64_t q_heads, uint64_t kv_heads, uint64_t head_dim,
+                                                        uint64_t first, uint64_t rows, unsigned int* over) {
+    if (!heads_ok("attention_causal_mix", q_heads, kv_heads, head_dim, rows)) return;
+    Geom G = geom(kCausal, q_heads, kv_heads, head_dim);
+    G.first = first;
+    G.span = first + rows;
+    launch_mix(o, nullptr, p, v, G, rows, over);
+    check_launch("attention_causal_mix");
+}
+
+// gpu.cuh:189 — kernels.cuh:928-948
+SILVANN_EXPORT void silvann_gfx950_attention_scores_grouped(float* p, const uint16_t* q, const uint16_t* k,
+                                                            uint64_t q_heads, uint64_t kv_heads, uint64_t head_dim,
+                                                            uint64_t length) {
+    if (!heads_ok("attention_scores_grouped", q_heads, kv_heads, head_dim, 1)) return;
+    Geom G = geom(kSingle, q_heads, kv_heads, head_dim);
+    G.length = length;
+    launch_scores(p, q, k, G, 1, length);
+    check_launch("attention_scores_grouped");
+}
+
+// gpu.cuh:190 — kernels.cuh:1095-1097
+SILVANN_EXPORT void silvann_gfx950_attention_softmax_rows(float* p, uint64_t rows, uint64_t length) {
+    Geom G = geom(kSingle, 1, 1, 1);   // row r at r·length, `length` long: the one-query geometry
+    G.length = length;
+    if (length == 0) return;
+    launch_softmax(p, nullptr, G, rows);
+    check_launch("attention_softmax_rows");
+}
+
+// gpu.cuh:191 — kernels.cuh:1028-1061
+SILVANN_EXPORT void silvann_gfx950_attention_causal_scores_grouped(float* p, const uint16_t* q, const uint16_t* k,
+                                                                   uint64_t q_heads, uint64_t kv_heads,
+                                                                   uint64_t head_dim, uint64_t first, uint64_t rows) {
+    if (!heads_ok("attention_causal_scores_grouped", q_heads, kv_heads, head_dim, rows)) return;
+    Geom G = geom(kCausal, q_heads, kv_heads, head_dim);
+    G.first = first;
+    G.span = first + rows;
+    launch_scores(p, q, k, G, rows, first + rows);
+    check_launch("attention_causal_scores_grouped");
+}
+
+// gpu.cuh:192 — kernels.cuh:1065-1081
+SILVANN_EXPORT void silvann_gfx950_attention_causal_softmax(float* p, uint64_t q_heads, uint64_t first, uint64_t rows) {
+    if (q_heads == 0) return;
+    Geom G = geom(kCausal, q_heads, 1, 1);
+    G.first = first;
+    G.span = first + rows;
+    launch_softmax(p, nullptr, G, rows * q_heads);
+    check_launch("attention_causal_softmax");
+}
+
+// gpu.cuh:195 — doors.cuh:417-424
+SILVANN_EXPORT void silvann_gfx950_attention_weights_rows(float* p, float* res, const uint16_t* q, const uint16_t* k,
+                                                          uint64_t q_heads, uint64_t kv_heads, uint64_t head_dim,
+                                                          uint64_t first, uint64_t rows) {
+    if (!heads_ok("attention_weights_rows", q_heads, kv_heads, head_dim, rows)) return;
+    Geom G = geom(kByRow, q_heads, kv_heads, head_dim);
+    G.first = first;
+    G.span = first + rows;
+    launch_scores(p, q, k, G, rows, first + rows);
+    launch_softmax(p, res, G, rows * q_heads);
+    check_launch("attention_weights_rows");
+}
+
+// gpu.cuh:196 — doors.cuh:425-432
+SILVANN_EXPORT void silvann_gfx950_attention_residual_mix_rows(float* res, const float* p, const uint16_t* v,
+                                                               uint64_t q_heads, uint64_t kv_heads, uint64_t head_dim,
+                                                               uint64_t first, uint64_t rows) {
+    if (!heads_ok("attention_residual_mix_rows", q_heads, kv_heads, head_dim, rows)) return;
+    Geom G = geom(kByRow, q_heads, kv_heads, head_dim);
+    G.first = first;
+    G.span = first + rows;
+    launch_mix(nullptr, res, p, v, G, rows, nullptr);
+    check_launch("attention_residual_mix_rows");
+}
+
+// gpu.cuh:222 — kernels.cuh:953-972
+SILVANN_EXPORT void silvann_gfx950_attention_scores_grouped_rows(float* p, uint64_t p_row, const uint16_t* q,
+                                                                 uint64_t q_row, const uint16_t* k, uint64_t k_row,
+                                                                 const uint32_t* lens, uint64_t q_heads,
+                                                                 uint64_t kv_heads, uint64_t head_dim, uint64_t most,
+                                                                 uint64_t rows) {
+    if (!heads_ok("attention_scores_grouped_rows", q_heads, kv_heads, head_dim, rows)) return;
+    Geom G = geom(kLens, q_heads, kv_heads, head_dim);
+    G.p_row = p_row; G.q_row = q_row; G.k_row = k_row; G.lens = lens;
+    launch_scores(p, q, k, G, rows, most);
+    check_launch("attention_scores_grouped_rows");
+}
+
+// gpu.cuh:223 — kernels.cuh:1104-1110
+SILVANN_EXPORT void silvann_gfx950_attention_softmax_lens(float* p, uint64_t p_row, const uint32_t* lens,
+                                                          uint64_t heads, uint64_t rows) {
+    if (heads == 0) return;
+    Geom G = geom(kLens, heads, 1, 1);
+    G.p_row = p_row; G.lens = lens;
+    launch_softmax(p, nullptr, G, rows * heads);
+    check_launch("attention_softmax_lens");
+}
+
+// gpu.cuh:224 — kernels.cuh:1169-1178
+SILVANN_EXPORT void silvann_gfx950_attention_mix_rows(uint16_t* o, uint64_t o_row, const float* p, uint64_t p_row,
+                                                      const uint16_t* v, uint64_t v_row, const uint32_t* lens,
+                                                      uint64_t q_heads, uint64_t kv_heads, uint64_t head_dim,
+                                                      uint64_t rows, unsigned int* over) {
+    if (!heads_ok("attention_mix_rows", q_heads, kv_heads, head_dim, rows)) return;
+    Geom G = geom(kLens, q_heads, kv_heads, head_dim);
+    G.p_row = p_row; G.k_row = v_row; G.o_row = o_row; G.lens = lens;
+    launch_mix(o, nullptr, p, v, G, rows, over);
+    check_launch("attention_mix_rows");
+}

@@ -1,0 +1,109 @@
+// library.hip — the library's control entry points: which stream a thread's doors are queued on, the
+// remembered launch failure, and the build's name.
+#include <stdio.h>
+#include <string.h>
+
+#include <vector>
+
+#include "common.hpp"
+#include "../../include/silvann_gfx950_attention.h"
+
+namespace silvann {
+
+// A door runs on its caller's thread, a worker's runner thread bound to its device (reference
+// engine/src/engine/launch.cuh:51-60), so the stream and the failure flag are the thread's own.
+static thread_local hipStream_t tls_stream = nullptr;
+static thread_local int tls_failed = 0;
+
+hipStream_t stream() { return tls_stream; }
+
+void check_launch(const char* what) {
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) {
+        fprintf(stderr, "silvann_gfx950: launch of %s failed: %s\n", what, hipGetErrorString(e));
+        tls_failed = 1;
+    }
+}
+
+struct Prof {
+    bool on = false;
+    std::vector<hipEvent_t> free_events;
+    std::vector<std::pair<hipEvent_t, hipEvent_t>> done[kProfKernels];
+    hipEvent_t open[kProfKernels] = {};
+};
+static thread_local Prof tls_prof;
+
+static hipEvent_t prof_event() {
+    Prof& P = tls_prof;
+    if (!P.free_events.empty()) {
+        hipEvent_t e = P.free_events.back();
+        P.free_events.pop_back();
+        return e;
+    }
+    hipEvent_t e = nullptr;
+    if (hipEventCreate(&e) != hipSuccess) return nullptr;
+    return e;
+}
+
+void prof_begin(int kernel) {
+    Prof& P = tls_prof;
+    if (!P.on) return;
+    hipEvent_t e = prof_event();
+    if (e && hipEventRecord(e, tls_stream) == hipSuccess) P.open[kernel] = e;
+}
+
+void prof_end(int kernel) {
+    Prof& P = tls_prof;
+    if (!P.on || !P.open[kernel]) return;
+    hipEvent_t e = prof_event();
+    if (e && hipEventRecord(e, tls_stream) == hipSuccess) P.done[kernel].push_back({P.open[kernel], e});
+    P.open[kernel] = nullptr;
+}
+
+void refuse(const char* what) {
+    fprintf(stderr, "silvann_gfx950: %s refused its operands\n", what);
+    tls_failed = 1;
+}
+
+}  // namespace silvann
+
+SILVANN_EXPORT void silvann_gfx950_set_stream(void* s) { silvann::tls_stream = (hipStream_t)s; }
+SILVANN_EXPORT void* silvann_gfx950_get_stream(void) { return (void*)silvann::tls_stream; }
+SILVANN_EXPORT int silvann_gfx950_launch_failed(void) {
+    int f = silvann::tls_failed;
+    silvann::tls_failed = 0;
+    return f;
+}
+static int prof_index(const char* kernel) {
+    static const char* names[silvann::kProfKernels] = {"decode_split", "decode_merge", "causal_mfma"};
+    for (int i = 0; i < silvann::kProfKernels; ++i)
+        if (kernel && strcmp(kernel, names[i]) == 0) return i;
+    return -1;
+}
+
+SILVANN_EXPORT void silvann_gfx950_profile_enable(int on) { silvann::tls_prof.on = on != 0; }
+
+SILVANN_EXPORT int silvann_gfx950_profile_read(const char* kernel, double* total_ms, uint64_t* launches) {
+    const int k = prof_index(kernel);
+    if (k < 0) return -1;
+    silvann::Prof& P = silvann::tls_prof;
+    double sum = 0.0;
+    uint64_t n = 0;
+    for (auto& pr : P.done[k]) {
+        float ms = 0.0f;
+        if (hipEventSynchronize(pr.second) != hipSuccess) return -1;
+        if (hipEventElapsedTime(&ms, pr.first, pr.second) != hipSuccess) return -1;
+        sum += ms;
+        ++n;
+        P.free_events.push_back(pr.first);
+        P.free_events.push_back(pr.second);
+    }
+    P.done[k].clear();
+    if (total_ms) *total_ms = sum;
+    if (launches) *launches = n;
+    return 0;
+}
+
+SILVANN_EXPORT const char* silvann_gfx950_version(void) {
+    return "gfx950 decode-splitk-mfma16 causal-mfma32 doors-17 v1";
+}

@@ -1,0 +1,194 @@
+"""The host side of the reference's attention verbs, over this library's doors.
+
+Each verb checks its operands the way the reference's verb does and refuses with the same fault word,
+then calls the doors in the same order with the same pointers (packages/nn/cpu/opcodes/attention__abi.cuh).
+A buffer is a torch tensor on the GPU; its "room" is its size in halves, as `nn__primitives__room` counts
+(packages/nn/cpu/primitives__header.cuh:38-55). Integers are Python ints. A refusal raises `Fault`
+carrying the word; nothing is launched.
+
+The two paged verbs are new (the reference has no page table): `decode_paged` and `causal_paged`, the
+split-K decode and the fused causal prefill, with the same kind of checks.
+"""
+from __future__ import annotations
+
+import torch
+
+from . import doors
+
+FAULT_TYPE = 0x4F504354      # "OPCT" packages/sys/contracts/objects/opcodes.cuh:6
+FAULT_BOUNDS = 0x4E50424E    # "NPBN" packages/nn/contracts/objects/primitives.cuh:5
+FAULT_OVERFLOW = 0x4E504F56  # "NPOV" primitives.cuh:57
+FAULT_ROOM = 0x4E41524D      # "NARM" packages/nn/contracts/objects/attention.cuh:46
+DIM_MAX = 1 << 20            # attention__abi.cuh:28 NN__ATTENTION__DIM_MAX
+ELEMENT_BYTES = 2            # primitives.cuh:82
+
+
+class Fault(RuntimeError):
+    def __init__(self, word: int):
+        self.word = word
+        super().__init__(f"fault {word.to_bytes(4, 'big').decode(errors='replace')} (0x{word:08X})")
+
+
+def word(name: str) -> int:
+    return int.from_bytes(name.encode(), "big")
+
+
+def room(t: torch.Tensor) -> int:
+    return t.numel() * t.element_size() // ELEMENT_BYTES
+
+
+def _dim(x) -> int:
+    """attention__abi.cuh:30-34: an integer in (0, DIM_MAX]."""
+    if not isinstance(x, int) or isinstance(x, bool) or x == 0 or x > DIM_MAX or x < 0:
+        raise Fault(FAULT_TYPE)
+    return x
+
+
+def _fits(n: int, r: int) -> bool:
+    return n <= r
+
+
+def check_fault(over: torch.Tensor) -> None:
+    """Raise the fault a door left in the fault word, as the engine does at the next apply."""
+    w = int(over.view(torch.int32)[0].item()) & 0xFFFFFFFF
+    if w:
+        raise Fault(w)
+
+
+def decode(q, k, v, scores, out, q_heads, kv_heads, head_dim, from_, to, over):
+    """`(nn__attention__decode q k v scores out q_heads kv_heads head_dim from to)` — attention__abi.cuh:129-160."""
+    q_heads, kv_heads, head_dim, to = _dim(q_heads), _dim(kv_heads), _dim(head_dim), _dim(to)
+    if not isinstance(from_, int) or from_ < 0:
+        raise Fault(FAULT_TYPE)
+    row = kv_heads * head_dim
+    if from_ >= to:
+        raise Fault(FAULT_BOUNDS)
+    length, cached = to - from_, to * row
+    if (q_heads % kv_heads or not _fits(q_heads * head_dim, room(q)) or not _fits(q_heads * head_dim, room(out))
+            or not _fits(cached, room(k)) or not _fits(cached, room(v))
+            or not _fits(2 * q_heads * length, room(scores))):
+        raise Fault(FAULT_BOUNDS)
+    skip = from_ * row * ELEMENT_BYTES
+    doors.attention_scores(scores, q, k.data_ptr() + skip, q_heads, kv_heads, head_dim, length)
+    doors.attention_mix(out, scores, v.data_ptr() + skip, q_heads, kv_heads, head_dim, length, over)
+    return out
+
+
+def _residual_fits(t, q_heads, head_dim) -> bool:
+    return _fits(2 * q_heads * (head_dim + 2), room(t))
+
+
+def residual(q, k, v, scores, res, q_heads, kv_heads, head_dim, from_, to):
+    """`(nn__attention__residual …)` — attention__abi.cuh:177-208."""
+    q_heads, kv_heads, head_dim, to = _dim(q_heads), _dim(kv_heads), _dim(head_dim), _dim(to)
+    if not isinstance(from_, int) or from_ < 0:
+        raise Fault(FAULT_TYPE)
+    row = kv_heads * head_dim
+    if from_ >= to:
+        raise Fault(FAULT_BOUNDS)
+    length, cached = to - from_, to * row
+    if (q_heads % kv_heads or not _fits(q_heads * head_dim, room(q)) or not _fits(cached, room(k))
+            or not _fits(cached, room(v)) or not _fits(2 * q_heads * length, room(scores))
+            or not _residual_fits(res, q_heads, head_dim)):
+        raise Fault(FAULT_BOUNDS)
+    skip = from_ * row * ELEMENT_BYTES
+    doors.attention_weights(scores, res, q, k.data_ptr() + skip, q_heads, kv_heads, head_dim, length)
+    doors.attention_residual_mix(res, scores, v.data_ptr() + skip, q_heads, kv_heads, head_dim, length)
+    return res
+
+
+def merge(a, b, into, q_heads, head_dim):
+    """`(nn__attention__merge a b into q_heads head_dim)` — attention__abi.cuh:212-227."""
+    q_heads, head_dim = _dim(q_heads), _dim(head_dim)
+    if not (_residual_fits(a, q_heads, head_dim) and _residual_fits(b, q_heads, head_dim)
+            and _residual_fits(into, q_heads, head_dim)):
+        raise Fault(FAULT_BOUNDS)
+    doors.attention_merge(into, a, b, q_heads, head_dim)
+    return into
+
+
+def finish(res, out, q_heads, head_dim, over):
+    """`(nn__attention__finish res out q_heads head_dim)` — attention__abi.cuh:230-243."""
+    q_heads, head_dim = _dim(q_heads), _dim(head_dim)
+    if not _residual_fits(res, q_heads, head_dim) or not _fits(q_heads * head_dim, room(out)):
+        raise Fault(FAULT_BOUNDS)
+    doors.attention_finish(out, res, q_heads, head_dim, over)
+    return out
+
+
+def rows_attention(q, keys, values, scores, att, q_heads, kv_heads, head_dim, first, rows, over):
+    """The attention of `nn__attention__rows` (attention__abi.cuh:345-421, the part at 370 and 407-414):
+    queries `q` for positions first .. first+rows-1 (their keys and values already in the cache) attend the
+    cache causally, as many rows a pass as the scores' room holds — causal_scores_grouped, causal_softmax,
+    causal_mix — into `att`. The verb's own limits on the whole layer (ROWS_MAX, the 512-blocks) belong to its
+    projections and are not this part's."""
+    q_heads, kv_heads, head_dim = _dim(q_heads), _dim(kv_heads), _dim(head_dim)
+    if not isinstance(first, int) or first < 0 or first >= (1 << 32) or not isinstance(rows, int) or rows <= 0:
+        raise Fault(word("NATB"))
+    qw, kvw, to = q_heads * head_dim, kv_heads * head_dim, first + rows
+    if head_dim % 2 or q_heads % kv_heads:
+        raise Fault(word("NATB"))
+    if (not _fits(rows * qw, room(q)) or not _fits(rows * qw, room(att)) or not _fits(to * kvw, room(keys))
+            or not _fits(to * kvw, room(values)) or scores.numel() * scores.element_size() // 4 < q_heads * to):
+        raise Fault(FAULT_ROOM)
+    per = scores.numel() * scores.element_size() // 4 // (q_heads * to)
+    npass = min(rows, per)
+    r0 = 0
+    while r0 < rows:
+        n = min(npass, rows - r0)
+        doors.attention_causal_scores_grouped(scores, q.data_ptr() + 2 * r0 * qw, keys, q_heads, kv_heads, head_dim,
+                                              first + r0, n)
+        doors.attention_causal_softmax(scores, q_heads, first + r0, n)
+        doors.attention_causal_mix(att.data_ptr() + 2 * r0 * qw, scores, values, q_heads, kv_heads, head_dim,
+                                   first + r0, n, over)
+        r0 += n
+    return att
+
+
+def decode_paged_scratch_bytes(q_heads, kv_heads, head_dim, most, rows) -> int:
+    return int(doors.attention_decode_paged_scratch(q_heads, kv_heads, head_dim, most, rows))
+
+
+def decode_paged(q, k, v, pages, lens, out, q_heads, kv_heads, head_dim, most, page_size=0, pages_row=0, k_row=0,
+                 scratch=None, over=None):
+    """One query position a row over its own (paged) cache — the split-K decode door. `pages` None: each row's
+    cache is contiguous at k + u·k_row. `lens` a uint32 GPU tensor of the rows' lengths, `most` ≥ every one."""
+    q_heads, kv_heads, head_dim, most = _dim(q_heads), _dim(kv_heads), _dim(head_dim), _dim(most)
+    rows = lens.numel()
+    if rows == 0 or q_heads % kv_heads or head_dim not in (64, 128, 256):
+        raise Fault(FAULT_BOUNDS)
+    if not _fits(rows * q_heads * head_dim, room(q)) or not _fits(rows * q_heads * head_dim, room(out)):
+        raise Fault(FAULT_BOUNDS)
+    if pages is not None:
+        if page_size <= 0 or page_size % 32 or pages_row * (rows - 1) + (most + page_size - 1) // page_size > pages.numel():
+            raise Fault(FAULT_BOUNDS)
+    need = decode_paged_scratch_bytes(q_heads, kv_heads, head_dim, most, rows)
+    if scratch is None:
+        scratch = torch.empty(max(need, 4), dtype=torch.uint8, device=q.device)
+    elif scratch.numel() * scratch.element_size() < need:
+        raise Fault(FAULT_BOUNDS)
+    if over is None:
+        over = torch.zeros(1, dtype=torch.int32, device=q.device)
+    doors.attention_decode_paged(out, q, k, v, pages, pages_row, page_size, k_row, lens, q_heads, kv_heads, head_dim,
+                                 most, rows, scratch, over)
+    return out
+
+
+def causal_paged(q, k, v, pages, out, q_heads, kv_heads, head_dim, first, rows, page_size=0, over=None):
+    """Causal prefill of positions first .. first+rows-1 over the (paged) cache — the fused MFMA door."""
+    q_heads, kv_heads, head_dim = _dim(q_heads), _dim(kv_heads), _dim(head_dim)
+    if (not isinstance(first, int) or first < 0 or not isinstance(rows, int) or rows <= 0 or q_heads % kv_heads
+            or head_dim not in (64, 128, 256)):
+        raise Fault(FAULT_BOUNDS)
+    qw, kvw, to = q_heads * head_dim, kv_heads * head_dim, first + rows
+    if not _fits(rows * qw, room(q)) or not _fits(rows * qw, room(out)):
+        raise Fault(FAULT_BOUNDS)
+    if pages is None:
+        if not _fits(to * kvw, room(k)) or not _fits(to * kvw, room(v)):
+            raise Fault(FAULT_BOUNDS)
+    elif page_size <= 0 or page_size % 32 or (to + page_size - 1) // page_size > pages.numel():
+        raise Fault(FAULT_BOUNDS)
+    if over is None:
+        over = torch.zeros(1, dtype=torch.int32, device=q.device)
+    doors.attention_causal_paged(out, q, k, v, pages, page_size, q_heads, kv_heads, head_dim, first, rows, over)
+    return out

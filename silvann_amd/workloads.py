@@ -1,0 +1,185 @@
+"""The benchmark configurations' synthetic inputs, made the same way everywhere (tests, bench, smoke).
+
+Every array comes from one `numpy.random.default_rng(seed)` in a fixed order: the lengths (batched decode),
+the page permutation, then q, k, v as standard normals in float32 narrowed to float16. A cache is a pool of
+pages, `page_size` positions × kv_heads × head_dim halves a page; row u's logical page j is physical page
+`pages[u·pages_row + j]`. `page_size` 0 means a contiguous cache, as the reference keeps it.
+"""
+from __future__ import annotations
+
+from dataclasses import dataclass
+
+import numpy as np
+
+
+@dataclass
+class Decode:
+    name: str
+    q_heads: int
+    kv_heads: int
+    head_dim: int
+    lens: np.ndarray          # uint32 [rows]
+    page_size: int            # 0: contiguous, row u's cache at u·k_row halves
+    pages: np.ndarray | None  # uint32 [rows · pages_row]
+    pages_row: int
+    k_row: int
+    q: np.ndarray             # f16 [rows][q_heads][head_dim]
+    k: np.ndarray             # f16 pool
+    v: np.ndarray
+    seed: int = 0
+
+    @property
+    def rows(self) -> int:
+        return len(self.lens)
+
+    @property
+    def most(self) -> int:
+        return int(self.lens.max())
+
+    def kv_bytes(self) -> int:
+        """The algorithmic bytes: every cached position's K and V row of every kv head, once."""
+        return int(self.lens.astype(np.int64).sum()) * self.kv_heads * self.head_dim * 2 * 2
+
+    def io_bytes(self) -> int:
+        """Plus q and o (fp16) and the page-table entries read."""
+        qo = 2 * self.rows * self.q_heads * self.head_dim * 2
+        pt = 0 if self.pages is None else 4 * int(sum((int(l) + self.page_size - 1) // self.page_size for l in self.lens))
+        return self.kv_bytes() + qo + pt
+
+    def gathered(self, u: int):
+        """Row u's K and V as the reference keeps them: contiguous [position][kv_head][head_dim]."""
+        row = self.kv_heads * self.head_dim
+        n = int(self.lens[u])
+        if self.pages is None:
+            base = u * self.k_row
+            return self.k[base: base + n * row], self.v[base: base + n * row]
+        pos = np.arange(n)
+        phys = self.pages[u * self.pages_row + pos // self.page_size].astype(np.int64) * self.page_size + pos % self.page_size
+        idx = (phys[:, None] * row + np.arange(row)[None, :]).ravel()
+        return self.k[idx], self.v[idx]
+
+
+@dataclass
+class Causal:
+    name: str
+    q_heads: int
+    kv_heads: int
+    head_dim: int
+    first: int
+    rows: int
+    page_size: int
+    pages: np.ndarray | None
+    q: np.ndarray
+    k: np.ndarray
+    v: np.ndarray
+    seed: int = 0
+
+    def pairs(self) -> int:
+        """Unmasked (query, key) pairs: every row sees `first` prefix keys plus itself and the rows before."""
+        return self.rows * self.first + self.rows * (self.rows + 1) // 2
+
+    def flops(self) -> int:
+        """4·q_heads·head_dim a pair: QK^T and PV, a multiply and an add each."""
+        return 4 * self.q_heads * self.head_dim * self.pairs()
+
+    def kv_bytes(self) -> int:
+        return (self.first + self.rows) * self.kv_heads * self.head_dim * 2 * 2
+
+    def gathered(self):
+        row = self.kv_heads * self.head_dim
+        n = self.first + self.rows
+        if self.pages is None:
+            return self.k[: n * row], self.v[: n * row]
+        pos = np.arange(n)
+        phys = self.pages[pos // self.page_size].astype(np.int64) * self.page_size + pos % self.page_size
+        idx = (phys[:, None] * row + np.arange(row)[None, :]).ravel()
+        return self.k[idx], self.v[idx]
+
+
+def _normal(rng, n):
+    return rng.standard_normal(n, dtype=np.float32).astype(np.float16)
+
+
+def device_normal(n, seed, dev):
+    """N(0,1) halves made on the GPU from a seeded torch generator — the benchmark's fast path for large
+    pools (a different stream of numbers from the numpy one; both sides of a check use the same arrays)."""
+    import torch
+    g = torch.Generator(device=dev)
+    g.manual_seed(seed)
+    return torch.randn(n, generator=g, dtype=torch.float32, device=dev).half()
+
+
+def _qkv(rng, seed, dev, nq, nkv):
+    if dev is None:
+        return _normal(rng, nq), _normal(rng, nkv), _normal(rng, nkv)
+    return (device_normal(nq, 3 * seed + 1, dev), device_normal(nkv, 3 * seed + 2, dev),
+            device_normal(nkv, 3 * seed + 3, dev))
+
+
+def decode(name, q_heads, kv_heads, head_dim, lens, page_size=0, seed=0, permute=True, rng=None, dev=None) -> Decode:
+    rng = rng or np.random.default_rng(seed)
+    lens = np.asarray(lens, dtype=np.uint32)
+    rows, row = len(lens), kv_heads * head_dim
+    if page_size:
+        per = [(int(l) + page_size - 1) // page_size for l in lens]
+        pool = sum(per)
+        perm = rng.permutation(pool).astype(np.uint32) if permute else np.arange(pool, dtype=np.uint32)
+        pages_row = max(per)
+        pages = np.zeros(rows * pages_row, np.uint32)
+        at = 0
+        for u, n in enumerate(per):
+            pages[u * pages_row: u * pages_row + n] = perm[at: at + n]
+            at += n
+        slots, k_row = pool * page_size, 0
+    else:
+        pages, pages_row = None, 0
+        k_row = int(lens.max()) * row
+        slots = rows * int(lens.max())
+    q, k, v = _qkv(rng, seed, dev, rows * q_heads * head_dim, slots * row)
+    return Decode(name, q_heads, kv_heads, head_dim, lens, page_size, pages, pages_row, k_row, q, k, v, seed)
+
+
+def causal(name, q_heads, kv_heads, head_dim, first, rows, page_size=0, seed=0, permute=True, dev=None) -> Causal:
+    rng = np.random.default_rng(seed)
+    n, row = first + rows, kv_heads * head_dim
+    if page_size:
+        npages = (n + page_size - 1) // page_size
+        pages = rng.permutation(npages).astype(np.uint32) if permute else np.arange(npages, dtype=np.uint32)
+        slots = npages * page_size
+    else:
+        pages, slots = None, n
+    q, k, v = _qkv(rng, seed, dev, rows * q_heads * head_dim, slots * row)
+    return Causal(name, q_heads, kv_heads, head_dim, first, rows, page_size, pages, q, k, v, seed)
+
+
+# ── the BASELINE configurations ─────────────────────────────────────────────────────────────────────
+
+def config1(seed=1, dev=None) -> Decode:
+    """C1: single-sequence decode, 16 q / 2 kv heads, head_dim 256, 2,048 cached positions (contiguous)."""
+    return decode("decode_c1_16q2kv_hd256_len2048", 16, 2, 256, [2048], page_size=0, seed=seed, dev=dev)
+
+
+def config2(seed=2, dev=None) -> Decode:
+    """C2: 32 sequences, lengths U[1024, 32768] from the seed, 32 q / 4 kv, head_dim 128, 256-position pages,
+    each sequence's page table a slice of a seeded permutation of the pool."""
+    rng = np.random.default_rng(seed)
+    lens = rng.integers(1024, 32769, 32)
+    return decode("decode_c2_32seq_32q4kv_hd128_paged256", 32, 4, 128, lens, page_size=256, rng=rng, seed=seed, dev=dev)
+
+
+def config3(seed=3, dev=None) -> Causal:
+    """C3: causal prefill of 4,096 positions, no prefix, 16 q / 2 kv heads, head_dim 256."""
+    return causal("causal_c3_4096_16q2kv_hd256", 16, 2, 256, 0, 4096, page_size=0, seed=seed, dev=dev)
+
+
+def config4(seed=4, dev=None) -> Causal:
+    """C4: 2,048 new positions over a 100,000-position paged prefix (256-position pages, permuted)."""
+    return causal("causal_c4_2048_over_100000_16q2kv_hd256_paged256", 16, 2, 256, 100000, 2048, page_size=256, seed=seed, dev=dev)
+
+
+def config5(seed=5, dev=None) -> Decode:
+    """C5: one query over 262,144 cached positions in 1,024 permuted 256-position pages, 16 q / 2 kv, hd 256."""
+    return decode("decode_c5_16q2kv_hd256_len262144_paged256", 16, 2, 256, [262144], page_size=256, seed=seed, dev=dev)
+
+
+CONFIGS = {1: config1, 2: config2, 3: config3, 4: config4, 5: config5}
