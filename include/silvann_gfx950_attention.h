@@ -117,7 +117,8 @@ void silvann_gfx950_attention_mix_rows(uint16_t* o, uint64_t o_row, const float*
 
 /* One query position a row over its own cache: row u's q_heads at q + u·q_heads·head_dim attend positions
  * 0 .. lens[u]-1; out o + u·q_heads·head_dim. Split-K flash decoding: `scratch` holds the partial residuals,
- * `silvann_gfx950_attention_decode_paged_scratch` bytes (0 if it needs none). `most` is the largest lens[u]
+ * `silvann_gfx950_attention_decode_paged_scratch` bytes (0 if it needs none). `page_size` a multiple of 16
+ * positions (of 32 for the causal row). `most` is the largest lens[u]
  * (a bound the grid is sized by; lens[u] <= most is the caller's promise). A row with lens[u] == 0 answers 0.
  * Split-K form of the reference's decode verb (engine/src/packages/nn/cpu/opcodes/attention__abi.cuh:129-160),
  * many rows as `attention_scores_grouped_rows` (gpu.cuh:222) takes them. */

@@ -30,10 +30,9 @@
 namespace silvann {
 namespace {
 
-constexpr int kTile = 32;   // keys a wave takes a step
 constexpr int kWaves = 4;
 constexpr int kThreads = 64 * kWaves;
-constexpr uint32_t kMaxSplits = 8192;  // the merge keeps a weight a split in LDS
+constexpr uint32_t kMaxSplits = 65536;  // splits a row: the split grid's x extent stays small
 
 struct DecodeArgs {
     const uint16_t* q;
@@ -50,25 +49,42 @@ struct DecodeArgs {
     float* part;
 };
 
-// Where tile `t0` of row `u`, kv head `g` starts in a plane: through the page table, or contiguous.
-__device__ __forceinline__ const uint16_t* tile_base(const uint16_t* plane, const DecodeArgs& a, uint32_t u,
-                                                     uint32_t g, uint32_t t0, uint64_t row, int hd) {
+// Where the 16 keys from position `t` of row `u`, kv head `g` start in a plane: through the page table (a
+// page holds a multiple of 16 positions, so 16 keys from a multiple of 16 never straddle two), or contiguous.
+__device__ __forceinline__ const uint16_t* group_base(const uint16_t* plane, const DecodeArgs& a, uint32_t u,
+                                                      uint32_t g, uint32_t t, uint64_t row, int hd) {
     if (a.pages) {
-        const uint64_t phys = (uint64_t)a.pages[(uint64_t)u * a.pages_row + t0 / a.page_size] * a.page_size +
-                              t0 % a.page_size;
+        const uint32_t ps = (uint32_t)a.page_size;
+        const uint64_t phys = (uint64_t)a.pages[(uint64_t)u * a.pages_row + t / ps] * ps + t % ps;
         return plane + phys * row + (uint64_t)g * hd;
     }
-    return plane + (uint64_t)u * a.k_row + (uint64_t)t0 * row + (uint64_t)g * hd;
+    return plane + (uint64_t)u * a.k_row + (uint64_t)t * row + (uint64_t)g * hd;
 }
 
-template <int HD>
-__global__ __launch_bounds__(kThreads) void decode_split(DecodeArgs a) {
+// A value tile in LDS: 32 rows of HD halves, no padding (the direct-to-LDS load writes 16 bytes a lane,
+// consecutively). Row `key`'s 16-byte chunk `c` sits at chunk slot c ^ f(key), f(key) = 2·((key / 4) % 4):
+// the transposed read takes one dim from keys 4·grp + j of the four lane groups, and the swizzle puts the
+// four groups' chunks in different banks.
+__device__ __forceinline__ int vslot(int key, int chunk) { return chunk ^ (((key >> 2) & 3) << 1); }
+
+// Keys a wave takes a step: 32 KB of K and V (16 KB each) at every head width.
+constexpr int tile_keys(int hd) { return 8192 / hd; }
+// Cache policy of the streamed K/V loads: non-temporal (read once, kept out of the caches' way).
+constexpr int kCacheStream = 2;
+// Which of decode_split's cache-policy variants runs (SILVANN_GFX950_DECODE_VARIANT overrides).
+constexpr int kDefaultVariant = 2;
+
+// VARIANT bit 0: non-temporal K loads; bit 1: non-temporal value loads into LDS. GROUPED: pages shorter than
+// a tile, so each 16-key group of a tile is looked up on its own; otherwise one lookup a tile.
+template <int HD, int VARIANT, bool GROUPED>
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))) void decode_split(DecodeArgs a) {
+    constexpr int TK = tile_keys(HD);  // keys a wave takes a step: 32 KB of K and V whatever the head width
+    constexpr int MT = TK / 16;      // 16-key M tiles of S^T
     constexpr int KS = HD / 32;      // k-steps of the S^T MFMA (32 dims each)
     constexpr int NT = HD / 16;      // d-tiles of the O^T accumulator
-    constexpr int VP = HD + 16;      // LDS pitch of a staged value row, in halves (HD·2 + 32 bytes)
-    constexpr int VCH = HD / 16;     // 16-byte value chunks a lane loads a tile
+    constexpr int VCH = TK * HD / 512;  // 16-byte value chunks a lane brings in a tile
     constexpr int CPR = HD / 8;      // 16-byte chunks in one value row
-    constexpr int kStageBytes = kWaves * kTile * VP * 2;
+    constexpr int kStageBytes = kWaves * TK * HD * 2;
     constexpr int kMergeBytes = kWaves * 16 * HD * 4 + 2 * kWaves * 16 * 4;
     constexpr int kSmem = kStageBytes > kMergeBytes ? kStageBytes : kMergeBytes;
     __shared__ __attribute__((aligned(16))) unsigned char smem[kSmem];
@@ -100,37 +116,51 @@ __global__ __launch_bounds__(kThreads) void decode_split(DecodeArgs a) {
     f32x4 acc[NT];
 #pragma unroll
     for (int n = 0; n < NT; ++n) acc[n] = (f32x4)0.0f;
-    _Float16* vs = (_Float16*)smem + w * kTile * VP;
+    _Float16* vs = (_Float16*)smem + w * TK * HD;
 
-    const uint32_t ntiles = (end - start + kTile - 1) / kTile;
+    const uint32_t ntiles = (end - start + TK - 1) / TK;
+    constexpr int NG = GROUPED ? MT : 1;
+    // key `key` (< TK) of the current tile in a plane whose group bases are `gb`
+    auto at = [&](const uint16_t* const* gb, int key) -> const uint16_t* {
+        if constexpr (GROUPED) return gb[key >> 4] + (uint64_t)(key & 15) * row;
+        else return gb[0] + (uint64_t)key * row;
+    };
     for (uint32_t j = w; j < ntiles; j += kWaves) {
-        const uint32_t t0 = start + j * kTile;
-        const uint32_t nvalid = min((uint32_t)kTile, end - t0);
-        const uint16_t* kb = tile_base(a.k, a, u, g, t0, row, HD);
-        const uint16_t* vb = tile_base(a.v, a, u, g, t0, row, HD);
+        const uint32_t t0 = start + j * TK;
+        const uint32_t nvalid = min((uint32_t)TK, end - t0);
+        // the tile's bases: one page-table lookup a tile, or one a 16-key group when pages are shorter
+        const uint16_t* kg[NG];
+        const uint16_t* vg[NG];
+#pragma unroll
+        for (int p = 0; p < NG; ++p) {
+            kg[p] = group_base(a.k, a, u, g, t0 + 16 * p, row, HD);
+            vg[p] = group_base(a.v, a, u, g, t0 + 16 * p, row, HD);
+        }
 
         // K as the A operand: lane (col, grp) reads key 16·p + col, dims 32·ks + 8·grp .. +8. Keys past the
-        // split read key 0 of the tile (their scores are masked).
-        f16x8 kr[2][KS];
+        // split read key 0 of the tile (their scores are masked). Streamed once: non-temporal.
+        f16x8 kr[MT][KS];
 #pragma unroll
-        for (int p = 0; p < 2; ++p) {
+        for (int p = 0; p < MT; ++p) {
             const int key = 16 * p + col;
-            const uint16_t* kk = kb + (uint64_t)(key < (int)nvalid ? key : 0) * row;
+            const f16x8* kk = (const f16x8*)at(kg, key < (int)nvalid ? key : 0) + grp;
 #pragma unroll
-            for (int ks = 0; ks < KS; ++ks) kr[p][ks] = *(const f16x8*)(kk + 32 * ks + 8 * grp);
+            for (int ks = 0; ks < KS; ++ks) kr[p][ks] = (VARIANT & 1) ? __builtin_nontemporal_load(kk + 4 * ks) : kk[4 * ks];
         }
-        // V rows, 16 bytes a lane, consecutive lanes along a row.
-        f16x8 vr[VCH];
+        // V straight into LDS: the load of step i writes slots 64·i .. 64·i + 63, one a lane; slot (key, c)
+        // holds the row's chunk c ^ f(key). Keys past the split bring key 0 of the tile (weight 0).
 #pragma unroll
         for (int i = 0; i < VCH; ++i) {
-            const int c = lane + 64 * i, key = c / CPR, part = c % CPR;
-            vr[i] = *(const f16x8*)(vb + (uint64_t)(key < (int)nvalid ? key : 0) * row + 8 * part);
+            const int slot = lane + 64 * i, key = slot / CPR, c = vslot(key, slot % CPR);
+            const uint16_t* src = at(vg, key < (int)nvalid ? key : 0) + 8 * c;
+            __builtin_amdgcn_global_load_lds((const void*)src, (__attribute__((address_space(3))) void*)(vs + 64 * 8 * i),
+                                             16, 0, (VARIANT & 2) ? kCacheStream : 0);
         }
 
         // S^T: lane holds keys 16·p + 4·grp + r of head col.
-        float sv[8];
+        float sv[MT * 4];
 #pragma unroll
-        for (int p = 0; p < 2; ++p) {
+        for (int p = 0; p < MT; ++p) {
             f32x4 st = (f32x4)0.0f;
 #pragma unroll
             for (int ks = 0; ks < KS; ++ks) st = __builtin_amdgcn_mfma_f32_16x16x32_f16(kr[p][ks], qb[ks], st, 0, 0, 0);
@@ -142,46 +172,45 @@ __global__ __launch_bounds__(kThreads) void decode_split(DecodeArgs a) {
         }
         float mx = sv[0];
 #pragma unroll
-        for (int r = 1; r < 8; ++r) mx = fmaxf(mx, sv[r]);
+        for (int r = 1; r < MT * 4; ++r) mx = fmaxf(mx, sv[r]);
         mx = groups_max(mx);
         const float mnew = fmaxf(m, mx);
         const float corr = fast_exp(m - mnew);
         float lsum = 0.0f;
-        f16x8 pb;
+        // P^T as the B operand of k-step sp (32 keys): keys 32·sp + 4·grp + jj and 32·sp + 16 + 4·grp + jj —
+        // the S^T registers of M tiles 2·sp and 2·sp + 1
+        f16x8 pb[MT / 2];
 #pragma unroll
-        for (int r = 0; r < 8; ++r) {
+        for (int r = 0; r < MT * 4; ++r) {
             const float pr = fast_exp(sv[r] - mnew);
             lsum += pr;
-            pb[r] = (_Float16)pr;
+            pb[r / 8][r % 8] = (_Float16)pr;
         }
         l = l * corr + lsum;
         m = mnew;
 #pragma unroll
         for (int n = 0; n < NT; ++n) acc[n] *= corr;
 
-        // Stage the value tile, then read it transposed as the A operand: lane (col, grp) takes dim
-        // 16·n + col of keys 4·grp .. +4 and 16 + 4·grp .. +4 — the keys its P^T column holds.
-#pragma unroll
-        for (int i = 0; i < VCH; ++i) {
-            const int c = lane + 64 * i, key = c / CPR, part = c % CPR;
-            *(f16x8*)(vs + key * VP + 8 * part) = vr[i];
-        }
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        // The value tile landed (the direct loads count as vector memory); read it transposed as the A
+        // operand: lane (col, grp) takes dim 16·n + col of the keys its P^T column holds.
+        __builtin_amdgcn_s_waitcnt(0x0F70);   // vmcnt(0)
         __builtin_amdgcn_wave_barrier();
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 #pragma unroll
-        for (int n = 0; n < NT; ++n) {
-            f16x8 va;
+        for (int sp = 0; sp < MT / 2; ++sp)
 #pragma unroll
-            for (int jj = 0; jj < 8; ++jj) {
-                const int key = jj < 4 ? 4 * grp + jj : 16 + 4 * grp + (jj - 4);
-                va[jj] = vs[key * VP + 16 * n + col];
+            for (int n = 0; n < NT; ++n) {
+                const int d = 16 * n + col;
+                f16x8 va;
+#pragma unroll
+                for (int jj = 0; jj < 8; ++jj) {
+                    const int key = 32 * sp + (jj < 4 ? 4 * grp + jj : 16 + 4 * grp + (jj - 4));
+                    va[jj] = vs[(key * CPR + vslot(key, d >> 3)) * 8 + (d & 7)];
+                }
+                acc[n] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va, pb[sp], acc[n], 0, 0, 0);
             }
-            acc[n] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va, pb, acc[n], 0, 0, 0);
-        }
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        // every lane's reads of this tile are done before the next tile's loads overwrite it
+        __builtin_amdgcn_s_waitcnt(0xC07F);   // lgkmcnt(0)
         __builtin_amdgcn_wave_barrier();
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
     }
     l = groups_sum(l);
 
@@ -220,52 +249,77 @@ __global__ __launch_bounds__(kThreads) void decode_split(DecodeArgs a) {
     }
 }
 
+// Pass 2: a workgroup per (row, query head, 64 dims). The four waves take every fourth split; a lane holds
+// one dim's running sum over its wave's splits; the waves' sums meet in LDS. Every split's weight
+// e^(m_s - M) needs the head's largest m first, folded over the whole workgroup.
 template <int HD>
 __global__ __launch_bounds__(256) void decode_merge(uint16_t* o, const float* part, const uint32_t* lens,
                                                     uint32_t q_heads, uint32_t chunk, uint32_t nsplit,
                                                     unsigned int* over) {
-    __shared__ float wts[kMaxSplits];
     __shared__ float red[8];
+    __shared__ float accs[4][64];
+    __shared__ float ls[4];
     const uint32_t h = blockIdx.x, u = blockIdx.y;
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    const int d = blockIdx.z * 64 + lane;
     const uint32_t len = lens[u];
     uint16_t* out = o + ((uint64_t)u * q_heads + h) * HD;
     if (len == 0) {
-        for (int d = threadIdx.x; d < HD; d += blockDim.x) out[d] = 0;
+        if (w == 0) out[d] = 0;
         return;
     }
     const uint32_t ns = (len + chunk - 1) / chunk;
     const float* pr = part + ((uint64_t)u * q_heads + h) * nsplit * (HD + 2);
-    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
 
     float mx = -INFINITY;
-    for (uint32_t s = threadIdx.x; s < ns; s += blockDim.x) mx = fmaxf(mx, pr[(uint64_t)s * (HD + 2)]);
+    for (uint32_t s = threadIdx.x; s < ns; s += 256) mx = fmaxf(mx, pr[(uint64_t)s * (HD + 2)]);
     mx = wave_max(mx);
     if (lane == 0) red[w] = mx;
     __syncthreads();
     const float M = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
-    float lsum = 0.0f;
-    for (uint32_t s = threadIdx.x; s < ns; s += blockDim.x) {
-        const float f = fast_exp(pr[(uint64_t)s * (HD + 2)] - M);
-        wts[s] = f;
-        lsum += f * pr[(uint64_t)s * (HD + 2) + 1];
+
+    // eight splits a step, eight independent sums: the loads of a step are all in flight together
+    constexpr int U = 8;
+    float accu[U], lsu[U];
+#pragma unroll
+    for (int k = 0; k < U; ++k) accu[k] = lsu[k] = 0.0f;
+    uint32_t s = w;
+    for (; s + 4 * (U - 1) < ns; s += 4 * U) {
+#pragma unroll
+        for (int k = 0; k < U; ++k) {
+            const float* a = pr + (uint64_t)(s + 4 * k) * (HD + 2);
+            const float f = fast_exp(a[0] - M);
+            accu[k] += f * a[2 + d];
+            lsu[k] += f * a[1];
+        }
     }
-    lsum = wave_sum(lsum);
-    if (lane == 0) red[4 + w] = lsum;
+    for (; s < ns; s += 4) {
+        const float* a = pr + (uint64_t)s * (HD + 2);
+        const float f = fast_exp(a[0] - M);
+        accu[0] += f * a[2 + d];
+        lsu[0] += f * a[1];
+    }
+    float acc0 = 0.0f, acc1 = 0.0f, lsum = 0.0f;
+#pragma unroll
+    for (int k = 0; k < U; ++k) {
+        acc0 += accu[k];
+        lsum += lsu[k];
+    }
+    accs[w][lane] = acc0 + acc1;
+    if (lane == 0) ls[w] = lsum;
     __syncthreads();
-    const float L = red[4] + red[5] + red[6] + red[7];
+    if (w != 0) return;
+    const float L = ls[0] + ls[1] + ls[2] + ls[3];
+    const float acc = accs[0][lane] + accs[1][lane] + accs[2][lane] + accs[3][lane];
     bool hit = false;
-    for (int d = threadIdx.x; d < HD; d += blockDim.x) {
-        float acc = 0.0f;
-        for (uint32_t s = 0; s < ns; ++s) acc += wts[s] * pr[(uint64_t)s * (HD + 2) + 2 + d];
-        out[d] = to_half(acc / L, hit);
-    }
+    out[d] = to_half(acc / L, hit);
     if (hit) *over = kFaultOverflow;
 }
 
 // The split length: a multiple of the 4 waves' 32-key tiles, sized so the grid is about 1024 workgroups
 // over the rows' longest length, and at most kMaxSplits splits a row. SILVANN_GFX950_DECODE_CHUNK overrides.
-uint32_t choose_chunk(uint64_t kv_heads, uint64_t hblocks, uint64_t most, uint64_t rows) {
-    const uint64_t step = (uint64_t)kTile * kWaves;
+uint32_t choose_chunk(uint64_t head_dim, uint64_t kv_heads, uint64_t hblocks, uint64_t most, uint64_t rows) {
+    const uint64_t step = (uint64_t)tile_keys((int)head_dim) * kWaves;
     if (const char* e = getenv("SILVANN_GFX950_DECODE_CHUNK")) {
         const uint64_t c = strtoull(e, nullptr, 10);
         if (c >= step) {
@@ -297,7 +351,7 @@ void decode_paged_launch(uint16_t* o, const uint16_t* q, const uint16_t* k, cons
                          uint64_t pages_row, uint64_t page_size, uint64_t k_row, const uint32_t* lens,
                          uint64_t q_heads, uint64_t kv_heads, uint64_t head_dim, uint64_t most, uint64_t rows,
                          float* scratch, unsigned int* over) {
-    if (!decode_shape_ok(q_heads, kv_heads, head_dim, most, rows) || (pages && (page_size == 0 || page_size % kTile))) {
+    if (!decode_shape_ok(q_heads, kv_heads, head_dim, most, rows) || (pages && (page_size == 0 || page_size % 16 || page_size > 0x7FFFFFFFull))) {
         fprintf(stderr, "silvann_gfx950: attention_decode_paged: unsupported shape (q_heads %llu kv_heads %llu "
                         "head_dim %llu most %llu rows %llu page_size %llu)\n",
                 (unsigned long long)q_heads, (unsigned long long)kv_heads, (unsigned long long)head_dim,
@@ -310,18 +364,30 @@ void decode_paged_launch(uint16_t* o, const uint16_t* q, const uint16_t* k, cons
     a.lens = lens;
     a.q_heads = (uint32_t)q_heads; a.kv_heads = (uint32_t)kv_heads; a.group = (uint32_t)(q_heads / kv_heads);
     a.hblocks = head_blocks(q_heads, kv_heads);
-    a.chunk = choose_chunk(kv_heads, a.hblocks, most, rows);
+    a.chunk = choose_chunk(head_dim, kv_heads, a.hblocks, most, rows);
     a.nsplit = (uint32_t)((most + a.chunk - 1) / a.chunk);
     a.scale = 1.0f / sqrtf((float)head_dim);
     a.part = scratch;
     const dim3 grid(a.nsplit, (uint32_t)(kv_heads * a.hblocks), (uint32_t)rows);
-    const dim3 mgrid((uint32_t)q_heads, (uint32_t)rows);
+    const dim3 mgrid((uint32_t)q_heads, (uint32_t)rows, (uint32_t)(head_dim / 64));
     hipStream_t st = stream();
+    static const int variant = [] {
+        const char* e = getenv("SILVANN_GFX950_DECODE_VARIANT");
+        return e ? (int)(strtol(e, nullptr, 10) & 3) : kDefaultVariant;
+    }();
+    const bool grouped = pages && page_size % tile_keys((int)head_dim) != 0;
     prof_begin(kProfDecodeSplit);
-    switch (head_dim) {
-        case 64: decode_split<64><<<grid, kThreads, 0, st>>>(a); break;
-        case 128: decode_split<128><<<grid, kThreads, 0, st>>>(a); break;
-        default: decode_split<256><<<grid, kThreads, 0, st>>>(a); break;
+    switch (head_dim * 4 + variant) {
+#define SILVANN_DECODE_CASE(HDV, VAR) \
+        case HDV * 4 + VAR: \
+            if (grouped) decode_split<HDV, VAR, true><<<grid, kThreads, 0, st>>>(a); \
+            else decode_split<HDV, VAR, false><<<grid, kThreads, 0, st>>>(a); \
+            break;
+        SILVANN_DECODE_CASE(64, 0) SILVANN_DECODE_CASE(64, 1) SILVANN_DECODE_CASE(64, 2) SILVANN_DECODE_CASE(64, 3)
+        SILVANN_DECODE_CASE(128, 0) SILVANN_DECODE_CASE(128, 1) SILVANN_DECODE_CASE(128, 2) SILVANN_DECODE_CASE(128, 3)
+        SILVANN_DECODE_CASE(256, 0) SILVANN_DECODE_CASE(256, 1) SILVANN_DECODE_CASE(256, 2) SILVANN_DECODE_CASE(256, 3)
+#undef SILVANN_DECODE_CASE
+        default: break;
     }
     prof_end(kProfDecodeSplit);
     prof_begin(kProfDecodeMerge);
@@ -336,7 +402,7 @@ void decode_paged_launch(uint16_t* o, const uint16_t* q, const uint16_t* k, cons
 
 uint64_t decode_paged_scratch(uint64_t q_heads, uint64_t kv_heads, uint64_t head_dim, uint64_t most, uint64_t rows) {
     if (!decode_shape_ok(q_heads, kv_heads, head_dim, most, rows)) return 0;
-    const uint32_t chunk = choose_chunk(kv_heads, head_blocks(q_heads, kv_heads), most, rows);
+    const uint32_t chunk = choose_chunk(head_dim, kv_heads, head_blocks(q_heads, kv_heads), most, rows);
     const uint64_t nsplit = (most + chunk - 1) / chunk;
     return rows * q_heads * nsplit * (head_dim + 2) * sizeof(float);
 }

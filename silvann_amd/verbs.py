@@ -160,7 +160,7 @@ def decode_paged(q, k, v, pages, lens, out, q_heads, kv_heads, head_dim, most, p
     if not _fits(rows * q_heads * head_dim, room(q)) or not _fits(rows * q_heads * head_dim, room(out)):
         raise Fault(FAULT_BOUNDS)
     if pages is not None:
-        if page_size <= 0 or page_size % 32 or pages_row * (rows - 1) + (most + page_size - 1) // page_size > pages.numel():
+        if page_size <= 0 or page_size % 16 or pages_row * (rows - 1) + (most + page_size - 1) // page_size > pages.numel():
             raise Fault(FAULT_BOUNDS)
     need = decode_paged_scratch_bytes(q_heads, kv_heads, head_dim, most, rows)
     if scratch is None:
