@@ -5,8 +5,12 @@
 // value once for all the query heads that share their kv head, and the reference's own residual contract
 // (kernels.cuh:1180-1267: per head [m, l, acc], merged exactly by e^(m_a - m), e^(m_b - m)) joins the splits:
 //
-//   pass 1  decode_split: a workgroup of 4 waves per (row, kv head, head block of up to 16 query heads,
-//           split of `chunk` positions). Each wave walks 32-key tiles of the split:
+//   plan    decode_plan: each row's split count, prefix-summed, and the work counter zeroed — in the
+//           scratch's header
+//   pass 1  decode_split: exactly as many workgroups of 4 waves as the chip holds at once; each takes work
+//           items — (split of `chunk` positions of a row, kv head, head block of up to 16 query heads) — from
+//           the counter until none are left, so rows of any lengths balance over the CUs. Each wave walks
+//           32 KB tiles of K and V (32 keys at head_dim 256, 64 at 128, 128 at 64) of the split:
 //             S^T = K · Q^T     v_mfma_f32_16x16x32_f16, keys as M, the group's query heads as N (a group of
 //                               8 fills half the columns; the other half is zero — the decode is HBM-bound,
 //                               and the MFMA has 50x the throughput it needs)
@@ -15,11 +19,12 @@
 //             O^T += V^T · P^T  the same MFMA, keys as K: P comes straight from the S^T registers, V^T from
 //                               the tile staged in LDS and read transposed
 //           then the four waves' (m, l, O) merge in LDS and the split's residual goes to `part`.
-//   pass 2  decode_merge: a workgroup per (row, query head) merges that head's split residuals and writes
+//   pass 2  decode_merge: a workgroup per (row, query head, 64 dims) merges that head's split residuals and writes
 //           acc / l as fp16, flagging overflow (kernels.cuh:1258-1267).
 //
-// K loads are 16 bytes a lane (8 halves of one key row: the MFMA A operand's own layout); V loads are
-// 16 bytes a lane with consecutive lanes on consecutive bytes of a row.
+// K loads are 16 bytes a lane (8 halves of one key row: the MFMA A operand's own layout) into registers; V
+// goes straight from HBM into LDS (16 bytes a lane, consecutive lanes on consecutive bytes of a row), so it
+// takes no registers and two workgroups fit on a CU at head_dim 256.
 #include <math.h>
 #include <stdio.h>
 #include <stdlib.h>
@@ -47,7 +52,43 @@ struct DecodeArgs {
     uint32_t chunk, nsplit;
     float scale;
     float* part;
+    const uint32_t* plan;   // plan[u]: splits of rows before u; plan[rows]: all splits
+    uint32_t* counter;      // the next work item
+    uint32_t rows;
 };
+
+// The scratch: the work counter, the plan, then the partial residuals [row][q head][split][head_dim + 2].
+constexpr uint64_t kPlanAt = 64;
+uint64_t part_at(uint64_t rows) { return (kPlanAt + 4 * (rows + 1) + 255) / 256 * 256; }
+
+// Each row's split count, prefix-summed into plan[0..rows], and the counter zeroed. One workgroup.
+__global__ __launch_bounds__(256) void decode_plan(const uint32_t* lens, uint32_t rows, uint32_t chunk, uint32_t* plan,
+                                                   uint32_t* counter) {
+    __shared__ uint32_t scan[256];
+    __shared__ uint32_t carry;
+    if (threadIdx.x == 0) {
+        counter[0] = 0;
+        carry = 0;
+    }
+    __syncthreads();
+    for (uint32_t base = 0; base < rows; base += 256) {
+        const uint32_t u = base + threadIdx.x;
+        const uint32_t n = u < rows ? (lens[u] + chunk - 1) / chunk : 0;
+        scan[threadIdx.x] = n;
+        __syncthreads();
+        for (int off = 1; off < 256; off <<= 1) {   // inclusive scan
+            const uint32_t add = threadIdx.x >= (unsigned)off ? scan[threadIdx.x - off] : 0;
+            __syncthreads();
+            scan[threadIdx.x] += add;
+            __syncthreads();
+        }
+        if (u < rows) plan[u] = carry + scan[threadIdx.x] - n;
+        __syncthreads();
+        if (threadIdx.x == 255) carry += scan[255];
+        __syncthreads();
+    }
+    if (threadIdx.x == 0) plan[rows] = carry;
+}
 
 // Where the 16 keys from position `t` of row `u`, kv head `g` start in a plane: through the page table (a
 // page holds a multiple of 16 positions, so 16 keys from a multiple of 16 never straddle two), or contiguous.
@@ -76,7 +117,9 @@ constexpr int kDefaultVariant = 2;
 
 // VARIANT bit 0: non-temporal K loads; bit 1: non-temporal value loads into LDS. GROUPED: pages shorter than
 // a tile, so each 16-key group of a tile is looked up on its own; otherwise one lookup a tile.
-template <int HD, int VARIANT, bool GROUPED>
+// PERSISTENT: the grid is what the chip holds at once and each workgroup takes items from the counter;
+// otherwise one workgroup an item (workgroup x is item x; past the last item it returns at once).
+template <int HD, int VARIANT, bool GROUPED, bool PERSISTENT>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))) void decode_split(DecodeArgs a) {
     constexpr int TK = tile_keys(HD);  // keys a wave takes a step: 32 KB of K and V whatever the head width
     constexpr int MT = TK / 16;      // 16-key M tiles of S^T
@@ -89,17 +132,33 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
     constexpr int kSmem = kStageBytes > kMergeBytes ? kStageBytes : kMergeBytes;
     __shared__ __attribute__((aligned(16))) unsigned char smem[kSmem];
 
-    const uint32_t s = blockIdx.x, u = blockIdx.z;
-    const uint32_t g = blockIdx.y / a.hblocks, hb = blockIdx.y % a.hblocks;
-    const uint32_t len = a.lens[u];
-    const uint32_t start = s * a.chunk;
-    if (start >= len) return;  // the whole workgroup: this split is past the row's length
-    const uint32_t end = min(len, start + a.chunk);
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
     const int col = lane & 15, grp = lane >> 4;
+    const uint64_t row = (uint64_t)a.kv_heads * HD;
+    const uint32_t GH = a.kv_heads * a.hblocks;
+    const uint32_t total = a.plan[a.rows] * GH;
+    __shared__ uint32_t item_at;
+    // the first item is the workgroup's own index; each next one comes from the counter (which counts past
+    // the grid), asked for at the start of an item and read at its end so the atomic's trip is hidden
+    uint32_t item = blockIdx.x;
+    for (;;) {
+    if (item >= total) break;
+    uint32_t next = 0;
+    if (PERSISTENT && threadIdx.x == 0) next = gridDim.x + atomicAdd(a.counter, 1u);
+    const uint32_t sidx = item / GH, gh = item % GH;
+    uint32_t lo = 0, hi = a.rows;
+    while (hi - lo > 1) {
+        const uint32_t mid = (lo + hi) >> 1;
+        if (a.plan[mid] <= sidx) lo = mid;
+        else hi = mid;
+    }
+    const uint32_t u = lo, s = sidx - a.plan[lo];
+    const uint32_t g = gh / a.hblocks, hb = gh % a.hblocks;
+    const uint32_t len = a.lens[u];
+    const uint32_t start = s * a.chunk;
+    const uint32_t end = min(len, start + a.chunk);
     const uint32_t h0 = g * a.group + hb * 16;
     const int nh = min(16, (int)(a.group - hb * 16));
-    const uint64_t row = (uint64_t)a.kv_heads * HD;
 
     // Q^T as the B operand: lane (col, grp) holds head col's dims 32·ks + 8·grp .. +8; heads past the block are 0.
     f16x8 qb[KS];
@@ -247,18 +306,26 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
             pr[1] = lsum;
         }
     }
+    if (!PERSISTENT) break;
+    if (threadIdx.x == 0) item_at = next;
+    __syncthreads();   // the merge area is read before the next item's tiles land in it; item_at is written
+    item = __builtin_amdgcn_readfirstlane(item_at);   // uniform: scalar registers
+    __syncthreads();   // every wave has read item_at before thread 0 writes the next
+    }
 }
 
-// Pass 2: a workgroup per (row, query head, 64 dims). The four waves take every fourth split; a lane holds
-// one dim's running sum over its wave's splits; the waves' sums meet in LDS. Every split's weight
-// e^(m_s - M) needs the head's largest m first, folded over the whole workgroup.
-template <int HD>
-__global__ __launch_bounds__(256) void decode_merge(uint16_t* o, const float* part, const uint32_t* lens,
-                                                    uint32_t q_heads, uint32_t chunk, uint32_t nsplit,
-                                                    unsigned int* over) {
-    __shared__ float red[8];
-    __shared__ float accs[4][64];
-    __shared__ float ls[4];
+// Pass 2: a workgroup of 4 or 16 waves (by the split count) per (row, query head, 64 dims). Wave w takes
+// splits w, w + waves, …, eight
+// at a time with eight independent sums (their loads in flight together); a lane holds one dim; the waves'
+// sums meet in LDS. Every split's weight e^(m_s - M) needs the head's largest m first, folded over the
+// whole workgroup.
+template <int HD, int kMergeWaves>
+__global__ __launch_bounds__(64 * kMergeWaves) void decode_merge(uint16_t* o, const float* part, const uint32_t* lens,
+                                                                 uint32_t q_heads, uint32_t chunk, uint32_t nsplit,
+                                                                 unsigned int* over) {
+    __shared__ float red[kMergeWaves];
+    __shared__ float accs[kMergeWaves][64];
+    __shared__ float ls[kMergeWaves];
     const uint32_t h = blockIdx.x, u = blockIdx.y;
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
     const int d = blockIdx.z * 64 + lane;
@@ -272,69 +339,93 @@ __global__ __launch_bounds__(256) void decode_merge(uint16_t* o, const float* pa
     const float* pr = part + ((uint64_t)u * q_heads + h) * nsplit * (HD + 2);
 
     float mx = -INFINITY;
-    for (uint32_t s = threadIdx.x; s < ns; s += 256) mx = fmaxf(mx, pr[(uint64_t)s * (HD + 2)]);
+    for (uint32_t s = threadIdx.x; s < ns; s += 64 * kMergeWaves) mx = fmaxf(mx, pr[(uint64_t)s * (HD + 2)]);
     mx = wave_max(mx);
     if (lane == 0) red[w] = mx;
     __syncthreads();
-    const float M = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    float M = red[0];
+#pragma unroll
+    for (int k = 1; k < kMergeWaves; ++k) M = fmaxf(M, red[k]);
 
-    // eight splits a step, eight independent sums: the loads of a step are all in flight together
     constexpr int U = 8;
     float accu[U], lsu[U];
 #pragma unroll
     for (int k = 0; k < U; ++k) accu[k] = lsu[k] = 0.0f;
     uint32_t s = w;
-    for (; s + 4 * (U - 1) < ns; s += 4 * U) {
+    for (; s + kMergeWaves * (U - 1) < ns; s += kMergeWaves * U) {
 #pragma unroll
         for (int k = 0; k < U; ++k) {
-            const float* a = pr + (uint64_t)(s + 4 * k) * (HD + 2);
+            const float* a = pr + (uint64_t)(s + kMergeWaves * k) * (HD + 2);
             const float f = fast_exp(a[0] - M);
             accu[k] += f * a[2 + d];
             lsu[k] += f * a[1];
         }
     }
-    for (; s < ns; s += 4) {
+    for (; s < ns; s += kMergeWaves) {
         const float* a = pr + (uint64_t)s * (HD + 2);
         const float f = fast_exp(a[0] - M);
         accu[0] += f * a[2 + d];
         lsu[0] += f * a[1];
     }
-    float acc0 = 0.0f, acc1 = 0.0f, lsum = 0.0f;
+    float acc = 0.0f, lsum = 0.0f;
 #pragma unroll
     for (int k = 0; k < U; ++k) {
-        acc0 += accu[k];
+        acc += accu[k];
         lsum += lsu[k];
     }
-    accs[w][lane] = acc0 + acc1;
+    accs[w][lane] = acc;
     if (lane == 0) ls[w] = lsum;
     __syncthreads();
     if (w != 0) return;
-    const float L = ls[0] + ls[1] + ls[2] + ls[3];
-    const float acc = accs[0][lane] + accs[1][lane] + accs[2][lane] + accs[3][lane];
+    float L = 0.0f, A = 0.0f;
+#pragma unroll
+    for (int k = 0; k < kMergeWaves; ++k) {
+        L += ls[k];
+        A += accs[k][lane];
+    }
     bool hit = false;
-    out[d] = to_half(acc / L, hit);
+    out[d] = to_half(A / L, hit);
     if (hit) *over = kFaultOverflow;
 }
 
-// The split length: a multiple of the 4 waves' 32-key tiles, sized so the grid is about 1024 workgroups
-// over the rows' longest length, and at most kMaxSplits splits a row. SILVANN_GFX950_DECODE_CHUNK overrides.
+// The split length: a multiple of the 4 waves' tiles, sized so the items (splits × kv heads × head blocks,
+// over the longest row for every row) about fill the chip once — more would re-pay the per-item merge,
+// fewer would leave CUs idle — and never past 1024 positions, past which the measured rate falls.
+// SILVANN_GFX950_DECODE_CHUNK overrides.
+uint64_t resident_groups();
 uint32_t choose_chunk(uint64_t head_dim, uint64_t kv_heads, uint64_t hblocks, uint64_t most, uint64_t rows) {
     const uint64_t step = (uint64_t)tile_keys((int)head_dim) * kWaves;
-    if (const char* e = getenv("SILVANN_GFX950_DECODE_CHUNK")) {
-        const uint64_t c = strtoull(e, nullptr, 10);
-        if (c >= step) {
-            uint64_t cc = (c + step - 1) / step * step;
-            while ((most + cc - 1) / cc > kMaxSplits) cc += step;
-            return (uint32_t)cc;
-        }
+    uint64_t c = 0;
+    if (const char* e = getenv("SILVANN_GFX950_DECODE_CHUNK")) c = strtoull(e, nullptr, 10);
+    if (c == 0) {
+        const uint64_t work = most * rows * kv_heads * hblocks;
+        c = (work + resident_groups() - 1) / resident_groups();
+        if (c > 1024) c = 1024;
     }
-    const uint64_t work = most * rows * kv_heads * hblocks;
-    uint64_t c = (work + 1023) / 1024;
     c = (c + step - 1) / step * step;
     if (c < step) c = step;
     while ((most + c - 1) / c > kMaxSplits) c += step;
-    if (c > 0xFFFFFFFFull - step) c = 0xFFFFFFFFull / step * step;
     return (uint32_t)c;
+}
+
+// Workgroups of decode_split the current device holds at once: two a CU (64 KB of LDS and two waves a SIMD
+// each). SILVANN_GFX950_DECODE_GROUPS overrides.
+uint64_t resident_groups() {
+    static thread_local int dev_cached = -1;
+    static thread_local uint64_t groups = 0;
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) dev = 0;
+    if (dev != dev_cached) {
+        int cus = 0;
+        if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0) cus = 256;
+        groups = 2ull * (uint64_t)cus;
+        if (const char* e = getenv("SILVANN_GFX950_DECODE_GROUPS")) {
+            const uint64_t g = strtoull(e, nullptr, 10);
+            if (g > 0) groups = g;
+        }
+        dev_cached = dev;
+    }
+    return groups;
 }
 
 uint32_t head_blocks(uint64_t q_heads, uint64_t kv_heads) { return (uint32_t)((q_heads / kv_heads + 15) / 16); }
@@ -367,8 +458,10 @@ void decode_paged_launch(uint16_t* o, const uint16_t* q, const uint16_t* k, cons
     a.chunk = choose_chunk(head_dim, kv_heads, a.hblocks, most, rows);
     a.nsplit = (uint32_t)((most + a.chunk - 1) / a.chunk);
     a.scale = 1.0f / sqrtf((float)head_dim);
-    a.part = scratch;
-    const dim3 grid(a.nsplit, (uint32_t)(kv_heads * a.hblocks), (uint32_t)rows);
+    a.counter = (uint32_t*)scratch;
+    a.plan = (const uint32_t*)((char*)scratch + kPlanAt);
+    a.part = (float*)((char*)scratch + part_at(rows));
+    a.rows = (uint32_t)rows;
     const dim3 mgrid((uint32_t)q_heads, (uint32_t)rows, (uint32_t)(head_dim / 64));
     hipStream_t st = stream();
     static const int variant = [] {
@@ -376,12 +469,30 @@ void decode_paged_launch(uint16_t* o, const uint16_t* q, const uint16_t* k, cons
         return e ? (int)(strtol(e, nullptr, 10) & 3) : kDefaultVariant;
     }();
     const bool grouped = pages && page_size % tile_keys((int)head_dim) != 0;
+    // as many workgroups as the chip holds at once (two a CU: LDS and registers allow no more), never more
+    // than there are work items
+    const uint64_t items = rows * a.nsplit * kv_heads * a.hblocks;   // at least the items there are
+    const dim3 pgrid((uint32_t)(items < resident_groups() ? items : resident_groups()));
+    const dim3 igrid((uint32_t)items);
+    static const int mode = [] {
+        const char* e = getenv("SILVANN_GFX950_DECODE_PERSISTENT");
+        return e ? (int)strtol(e, nullptr, 10) : -1;
+    }();
+    // measured: one workgroup an item beats the queue at both benchmark shapes (C2 5.17 vs 4.87 TB/s,
+    // C5 6.2 vs 5.1), so the queue is opt-in
+    const bool persistent = mode > 0;
+    decode_plan<<<1, 256, 0, st>>>(lens, a.rows, a.chunk, (uint32_t*)a.plan, a.counter);
     prof_begin(kProfDecodeSplit);
     switch (head_dim * 4 + variant) {
 #define SILVANN_DECODE_CASE(HDV, VAR) \
         case HDV * 4 + VAR: \
-            if (grouped) decode_split<HDV, VAR, true><<<grid, kThreads, 0, st>>>(a); \
-            else decode_split<HDV, VAR, false><<<grid, kThreads, 0, st>>>(a); \
+            if (persistent) { \
+                if (grouped) decode_split<HDV, VAR, true, true><<<pgrid, kThreads, 0, st>>>(a); \
+                else decode_split<HDV, VAR, false, true><<<pgrid, kThreads, 0, st>>>(a); \
+            } else { \
+                if (grouped) decode_split<HDV, VAR, true, false><<<igrid, kThreads, 0, st>>>(a); \
+                else decode_split<HDV, VAR, false, false><<<igrid, kThreads, 0, st>>>(a); \
+            } \
             break;
         SILVANN_DECODE_CASE(64, 0) SILVANN_DECODE_CASE(64, 1) SILVANN_DECODE_CASE(64, 2) SILVANN_DECODE_CASE(64, 3)
         SILVANN_DECODE_CASE(128, 0) SILVANN_DECODE_CASE(128, 1) SILVANN_DECODE_CASE(128, 2) SILVANN_DECODE_CASE(128, 3)
@@ -391,11 +502,16 @@ void decode_paged_launch(uint16_t* o, const uint16_t* q, const uint16_t* k, cons
     }
     prof_end(kProfDecodeSplit);
     prof_begin(kProfDecodeMerge);
+    const bool wide = a.nsplit > 64;
+#define SILVANN_MERGE(HDV) \
+    if (wide) decode_merge<HDV, 16><<<mgrid, 1024, 0, st>>>(o, a.part, lens, a.q_heads, a.chunk, a.nsplit, over); \
+    else decode_merge<HDV, 4><<<mgrid, 256, 0, st>>>(o, a.part, lens, a.q_heads, a.chunk, a.nsplit, over);
     switch (head_dim) {
-        case 64: decode_merge<64><<<mgrid, 256, 0, st>>>(o, scratch, lens, a.q_heads, a.chunk, a.nsplit, over); break;
-        case 128: decode_merge<128><<<mgrid, 256, 0, st>>>(o, scratch, lens, a.q_heads, a.chunk, a.nsplit, over); break;
-        default: decode_merge<256><<<mgrid, 256, 0, st>>>(o, scratch, lens, a.q_heads, a.chunk, a.nsplit, over); break;
+        case 64: SILVANN_MERGE(64) break;
+        case 128: SILVANN_MERGE(128) break;
+        default: SILVANN_MERGE(256) break;
     }
+#undef SILVANN_MERGE
     prof_end(kProfDecodeMerge);
     check_launch("attention_decode_paged");
 }
@@ -404,7 +520,7 @@ uint64_t decode_paged_scratch(uint64_t q_heads, uint64_t kv_heads, uint64_t head
     if (!decode_shape_ok(q_heads, kv_heads, head_dim, most, rows)) return 0;
     const uint32_t chunk = choose_chunk(head_dim, kv_heads, head_blocks(q_heads, kv_heads), most, rows);
     const uint64_t nsplit = (most + chunk - 1) / chunk;
-    return rows * q_heads * nsplit * (head_dim + 2) * sizeof(float);
+    return part_at(rows) + rows * q_heads * nsplit * (head_dim + 2) * sizeof(float);
 }
 
 }  // namespace silvann
