@@ -60,6 +60,18 @@ __device__ __forceinline__ float groups_sum(float v) {
     return v + __shfl_xor(v, 32);
 }
 
+// 16 bytes a lane from global memory straight into LDS: lane l's data lands at `lds` + 16·l (`lds` must be
+// the same for the whole wave). Written as its own instruction, not the builtin, so the compiler does not
+// make every later LDS read wait for it: the caller orders it with explicit vmcnt waits and barriers.
+__device__ __forceinline__ void dma16(const void* src, __attribute__((address_space(3))) void* lds) {
+    const uint32_t m0 = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)lds);
+    asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" : : "v"(src), "s"(m0) : "memory", "m0");
+}
+__device__ __forceinline__ void dma16_nt(const void* src, __attribute__((address_space(3))) void* lds) {
+    const uint32_t m0 = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)lds);
+    asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off nt" : : "v"(src), "s"(m0) : "memory", "m0");
+}
+
 // ── launch bookkeeping ─────────────────────────────────────────────────────────────────────────────
 hipStream_t stream();
 // Records a failed launch (printed once, remembered until silvann_gfx950_launch_failed reads it).
