@@ -65,11 +65,22 @@ __device__ __forceinline__ float groups_sum(float v) {
 // make every later LDS read wait for it: the caller orders it with explicit vmcnt waits and barriers.
 __device__ __forceinline__ void dma16(const void* src, __attribute__((address_space(3))) void* lds) {
     const uint32_t m0 = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)lds);
-    asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" : : "v"(src), "s"(m0) : "memory", "m0");
+    asm volatile("global_load_lds_dwordx4 %0, off" : : "v"(src), "{m0}"(m0) : "memory");
+}
+// The same from a wave-uniform base (scalar registers) plus a 32-bit per-lane byte offset: no 64-bit
+// address arithmetic in the vector unit.
+__device__ __forceinline__ void dma16s(const void* base, uint32_t off, __attribute__((address_space(3))) void* lds) {
+    const uint32_t m0 = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)lds);
+    const uint64_t b = (uint64_t)(uintptr_t)base;
+    // readfirstlane returns a signed int: widen through uint32_t, or the low word sign-extends over the high
+    const uint32_t lo = (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)b);
+    const uint32_t hi = (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)(b >> 32));
+    const uint64_t sb = ((uint64_t)hi << 32) | (uint64_t)lo;
+    asm volatile("global_load_lds_dwordx4 %0, %1" : : "v"(off), "s"(sb), "{m0}"(m0) : "memory");
 }
 __device__ __forceinline__ void dma16_nt(const void* src, __attribute__((address_space(3))) void* lds) {
     const uint32_t m0 = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)lds);
-    asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off nt" : : "v"(src), "s"(m0) : "memory", "m0");
+    asm volatile("global_load_lds_dwordx4 %0, off nt" : : "v"(src), "{m0}"(m0) : "memory");
 }
 
 // ── launch bookkeeping ─────────────────────────────────────────────────────────────────────────────

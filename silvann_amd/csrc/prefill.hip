@@ -41,13 +41,13 @@ struct CausalArgs {
     const uint16_t* k;
     const uint16_t* v;
     const uint32_t* pages;
-    uint64_t page_size;
+    uint32_t page_size;
     uint32_t q_heads, kv_heads, group;
     uint32_t hw;        // heads a workgroup (4, 2 or 1)
     uint32_t hblocks;   // group / hw
     uint32_t rt;        // rows a workgroup: 32 · (4 / hw)
     uint32_t rtiles;    // ceil(rows / rt)
-    uint64_t first, rows;
+    uint32_t first, rows;   // first + rows < 2^31: positions and key counts are 32-bit
     float scale_log2;   // 1/sqrt(head_dim) · log2(e)
     unsigned int* over;
 };
@@ -60,7 +60,7 @@ template <int CPR> __device__ __forceinline__ int vslot(int row, int c) {
     return c ^ ((row & (CPR >= 16 ? 3 : (CPR / 4 - 1))) << 2);
 }
 
-// Page-table entries a workgroup keeps in LDS (16 KB); a longer table is read from memory.
+// Page-table entries a workgroup keeps in LDS (16 KB); a longer table is read through the scalar cache.
 constexpr uint32_t kPagesInLds = 4096;
 
 template <int HD>
@@ -73,6 +73,23 @@ constexpr int kStages = 4;
 // accumulator is rescaled.
 constexpr float kRescale = 8.0f;
 
+typedef __attribute__((address_space(3))) void* lds_ptr;
+
+// A uniform 32-bit load through the scalar cache (a read; the page table is never written by the kernel).
+__device__ __forceinline__ uint32_t scalar_load(const uint32_t* p) {
+    uint32_t x;
+    asm volatile("s_load_dword %0, %1, 0x0\n\ts_waitcnt lgkmcnt(0)" : "=s"(x) : "s"(p) : "memory");
+    return x;
+}
+
+// x *= c for an accumulator element held in an accumulation register, in place.
+__device__ __forceinline__ void scale_acc(float& x, float c) {
+    float tmp;
+    asm volatile("v_accvgpr_read_b32 %1, %0\n\tv_mul_f32 %1, %1, %2\n\tv_accvgpr_write_b32 %0, %1"
+                 : "+a"(x), "=&v"(tmp)
+                 : "v"(c));
+}
+
 // PTL: the page table fits LDS (kPagesInLds entries) and tiles look their page up there.
 template <int HD, bool PAIRED, bool PTL>
 __global__ __launch_bounds__(kThreads) void causal_mfma(CausalArgs a) {
@@ -80,6 +97,7 @@ __global__ __launch_bounds__(kThreads) void causal_mfma(CausalArgs a) {
     constexpr int KSTEPS = HD / 16;    // k-steps of S^T (16 dims each)
     constexpr int DT = HD / 32;        // 32-dim tiles of O^T
     constexpr int LOADS = kKT * CPR / kThreads;   // 16-byte direct loads a thread issues a plane a tile
+    constexpr uint32_t RB = 2 * HD;    // bytes a key row in a stage
     __shared__ __attribute__((aligned(16))) Stage<HD> ring[kStages];
     __shared__ uint32_t pt[PTL ? kPagesInLds : 1];   // the sequence's page table, off the memory counter
 
@@ -87,51 +105,49 @@ __global__ __launch_bounds__(kThreads) void causal_mfma(CausalArgs a) {
     const int col = lane & 31, half = lane >> 5;
     const uint32_t g = blockIdx.y / a.hblocks, hb = blockIdx.y % a.hblocks;
     const uint32_t head = g * a.group + hb * a.hw + (w % a.hw);
-    const uint64_t row = (uint64_t)a.kv_heads * HD;
+    const uint32_t row = a.kv_heads * HD;   // elements a cache position
     bool hit = false;
 
-    // One 32-key tile of K and V into stage `st`: thread slot s = tid + 256·i is row s / CPR, physical chunk
-    // s % CPR, which holds logical chunk (s % CPR) ^ swizzle(row). Keys past `nkeys` bring key 0 of the
-    // tile (masked).
-    auto tile_row = [&](const uint16_t* plane, uint64_t t0) __attribute__((always_inline)) -> const uint16_t* {
-        if (!a.pages) return plane + t0 * row;
-        const uint32_t j = (uint32_t)(t0 / a.page_size);
-        uint32_t page;
-        if constexpr (PTL) page = pt[j];
-        else page = a.pages[j];
-        return plane + ((uint64_t)page * a.page_size + t0 % a.page_size) * row;
-    };
-    auto load_tile = [&](int st, uint32_t t, uint64_t nkeys) __attribute__((always_inline)) {
-        const uint64_t t0 = (uint64_t)t * kKT;
-        const uint16_t* kb = tile_row(a.k, t0) + (uint64_t)g * HD;
-        const uint16_t* vb = tile_row(a.v, t0) + (uint64_t)g * HD;
-        Stage<HD>& S = ring[st];
+    // Loop-invariant offsets. Direct loads: thread slot s = tid + 256·i is key row s / CPR, physical chunk
+    // s % CPR, which holds logical chunk (s % CPR) ^ swizzle(row) — byte offsets from the tile's key 0 (and
+    // from key 0 itself for the last tile's keys past the cache, which are masked).
+    uint32_t koff[LOADS], voff[LOADS];
 #pragma unroll
-        for (int i = 0; i < LOADS; ++i) {
-            const int s = tid + kThreads * i, r = s / CPR, pc = s % CPR;
-            const uint64_t rr = t0 + r < nkeys ? (uint64_t)r : 0;
-            dma16(kb + rr * row + 8 * kslot<CPR>(r, pc),
-                  (__attribute__((address_space(3))) void*)(&S.k[8 * kThreads * i + 8 * (tid & ~63)]));
-            dma16(vb + rr * row + 8 * vslot<CPR>(r, pc),
-                  (__attribute__((address_space(3))) void*)(&S.v[8 * kThreads * i + 8 * (tid & ~63)]));
+    for (int i = 0; i < LOADS; ++i) {
+        const int s = tid + kThreads * i, r = s / CPR, pc = s % CPR;
+        koff[i] = (uint32_t)r * row * 2u + 16u * kslot<CPR>(r, pc);
+        voff[i] = (uint32_t)r * row * 2u + 16u * vslot<CPR>(r, pc);
+    }
+    // S^T A operand: key row col, logical chunk 2·kk + half; the swizzle touches the chunk's low four bits,
+    // so k-steps kk and kk + 8 differ by 16 chunks (an immediate). O^T A operand (the transposing read), per
+    // dim tile n: lane 4·jj + rr of a 16-lane block points at key 4·half + jj (+ 16·s2 + 8·hh, immediates),
+    // dims d0 .. d0+3 with d0 = 32·n + 16·(block & 1) + 4·rr; the swizzle touches bits 2-3 of the chunk, so
+    // dim tiles n and n + 4 differ by 16 chunks.
+    constexpr int KR = KSTEPS < 8 ? KSTEPS : 8, VR = DT < 4 ? DT : 4;
+    uint32_t kread[KR], vread[VR];
+    {
+        const int blk = lane >> 4, li = lane & 15, jj = li >> 2, rr = li & 3, key = 4 * half + jj;
+#pragma unroll
+        for (int kk = 0; kk < KR; ++kk) kread[kk] = col * RB + 16u * kslot<CPR>(col, 2 * kk + half);
+#pragma unroll
+        for (int n = 0; n < VR; ++n) {
+            const int d0 = 32 * n + 16 * (blk & 1) + 4 * rr;
+            vread[n] = key * RB + 16u * vslot<CPR>(key, d0 >> 3) + 2u * (d0 & 7);
         }
-    };
+    }
 
     f32x16 acc[DT];
     f16x8 qb[KSTEPS];
 
-    // S^T (32 keys × 32 rows) of stage `st`: lane holds keys 8·(r/4) + 4·half + r%4 of row col; two chains.
+    // S^T (32 keys × 32 rows) of stage `st`: lane holds keys 8·(r/4) + 4·half + r%4 of row col.
     auto scores = [&](int st) __attribute__((always_inline)) -> f32x16 {
-        const Stage<HD>& S = ring[st];
-        f32x16 c0 = (f32x16)0.0f, c1 = (f32x16)0.0f;
+        const char* S = (const char*)ring[st].k;
+        f32x16 c = (f32x16)0.0f;
 #pragma unroll
-        for (int kk = 0; kk < KSTEPS; kk += 2) {
-            const f16x8 k0 = *(const f16x8*)(&S.k[col * HD + 8 * kslot<CPR>(col, 2 * kk + half)]);
-            const f16x8 k1 = *(const f16x8*)(&S.k[col * HD + 8 * kslot<CPR>(col, 2 * kk + 2 + half)]);
-            c0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(k0, qb[kk], c0, 0, 0, 0);
-            c1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(k1, qb[kk + 1], c1, 0, 0, 0);
-        }
-        return c0 + c1;
+        for (int kk = 0; kk < KSTEPS; ++kk)
+            c = __builtin_amdgcn_mfma_f32_32x32x16_f16(*(const f16x8*)(S + kread[kk % 8] + 256 * (kk / 8)), qb[kk], c,
+                                                        0, 0, 0);
+        return c;
     };
 
     // O^T (32 dims × 32 rows) += V^T · P^T for stage `st`, per dim tile n and k-step s2 (16 keys): the A
@@ -139,124 +155,171 @@ __global__ __launch_bounds__(kThreads) void causal_mfma(CausalArgs a) {
     // P^T holds. The transposing read: in each 16-lane block, lane 4·jj + rr points at row (key) jj, dims
     // d0 + 4·rr .. +3, and lane i gets that row's dim d0 + i; two reads (keys +0 and +8) make the 8 halves.
     auto mix = [&](int st, const f16x8* pb) __attribute__((always_inline)) {
-        const Stage<HD>& S = ring[st];
-        const int blk = lane >> 4, li = lane & 15, jj = li >> 2, rr = li & 3;
+        const char* S = (const char*)ring[st].v;
 #pragma unroll
         for (int s2 = 0; s2 < 2; ++s2)
 #pragma unroll
             for (int n = 0; n < DT; ++n) {
-                const int d0 = 32 * n + 16 * (blk & 1) + 4 * rr;
-                f16x8 va;
-#pragma unroll
-                for (int hh = 0; hh < 2; ++hh) {
-                    const int key = 16 * s2 + 8 * hh + 4 * half + jj;
-                    const _Float16* src = &S.v[key * HD + 8 * vslot<CPR>(key, d0 >> 3) + (d0 & 7)];
-                    const s16x4 x = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-                        (__attribute__((address_space(3))) s16x4*)(src));
-                    const f16x4 xh = __builtin_bit_cast(f16x4, x);
-                    va[4 * hh + 0] = xh[0];
-                    va[4 * hh + 1] = xh[1];
-                    va[4 * hh + 2] = xh[2];
-                    va[4 * hh + 3] = xh[3];
-                }
+                const s16x4 x0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                    (__attribute__((address_space(3))) s16x4*)(S + vread[n % 4] + 256 * (n / 4) + (16 * s2) * RB));
+                const s16x4 x1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                    (__attribute__((address_space(3))) s16x4*)(S + vread[n % 4] + 256 * (n / 4) + (16 * s2 + 8) * RB));
+                const f16x8 va = __builtin_bit_cast(f16x8, __builtin_shufflevector(x0, x1, 0, 1, 2, 3, 4, 5, 6, 7));
                 acc[n] = __builtin_amdgcn_mfma_f32_32x32x16_f16(va, pb[s2], acc[n], 0, 0, 0);
             }
     };
 
     auto process = [&](uint32_t rtile) __attribute__((always_inline)) {
-        const uint64_t r0 = (uint64_t)rtile * a.rt + (uint64_t)(w / a.hw) * 32;   // the wave's first row
-        const uint64_t wg_r0 = (uint64_t)rtile * a.rt;
-        const uint64_t wg_rlast = min(a.rows, wg_r0 + a.rt) - 1;
-        const uint64_t nkeys = a.first + wg_rlast + 1;             // keys the workgroup's last row sees
-        const uint32_t ntiles = (uint32_t)((nkeys + kKT - 1) / kKT);
-        const uint64_t myrow = r0 + col;
+        const uint32_t wg_r0 = rtile * a.rt;
+        const uint32_t r0 = wg_r0 + (w / a.hw) * 32;   // the wave's first row
+        const uint32_t wg_rlast = min(a.rows, wg_r0 + a.rt) - 1;
+        const uint32_t nkeys = a.first + wg_rlast + 1;   // keys the workgroup's last row sees
+        const uint32_t ntiles = (nkeys + kKT - 1) / kKT;
+        const uint32_t myrow = r0 + col;
         const bool row_ok = myrow < a.rows;
         {
-            const uint16_t* qr = a.q + ((row_ok ? myrow : 0) * a.q_heads + head) * HD;
+            const uint16_t* qr = a.q + ((uint64_t)(row_ok ? myrow : 0) * a.q_heads + head) * HD;
 #pragma unroll
             for (int kk = 0; kk < KSTEPS; ++kk) qb[kk] = *(const f16x8*)(qr + 16 * kk + 8 * half);
         }
-        const uint64_t mypos = a.first + (row_ok ? myrow : 0);
+        const uint32_t mypos = a.first + (row_ok ? myrow : 0);
+        const uint32_t diag_from = a.first + r0;   // tile t is diagonal for the wave when 32·t + 31 > diag_from
 #pragma unroll
         for (int n = 0; n < DT; ++n) acc[n] = (f32x16)0.0f;
         float m = -INFINITY, l = 0.0f;
+
+        // The load cursor: tiles are loaded in order, so the page and the offset in it advance by a tile
+        // each load (page_size is a multiple of the tile).
+        uint32_t lt = 0, lj = 0, loff = 0, page = 0;
+        auto load_tile = [&]() __attribute__((always_inline)) {
+            uint64_t base;   // elements from the plane's start to the tile's key 0, kv head g
+            if (!a.pages) {
+                base = (uint64_t)lt * kKT * row;
+            } else {
+                if (loff == 0) {
+                    if constexpr (PTL) page = __builtin_amdgcn_readfirstlane(pt[lj]);
+                    else page = scalar_load(a.pages + lj);
+                }
+                base = ((uint64_t)page * a.page_size + loff) * row;
+                loff += kKT;
+                if (loff == a.page_size) { loff = 0; ++lj; }
+            }
+            base += (uint64_t)g * HD;
+            const bool full = (lt + 1) * kKT <= nkeys;
+            char* S = (char*)&ring[lt % kStages];
+            ++lt;
+            const uint16_t* kb = a.k + base;
+            const uint16_t* vb = a.v + base;
+            if (full) {
+#pragma unroll
+                for (int i = 0; i < LOADS; ++i) {
+                    const uint32_t at = 16u * (kThreads * i + (tid & ~63));
+                    dma16s(kb, koff[i], (lds_ptr)(S + at));
+                    dma16s(vb, voff[i], (lds_ptr)(S + sizeof(_Float16) * kKT * HD + at));
+                }
+            } else {   // the last tile: keys past the cache bring the tile's key 0 (masked)
+                const uint32_t left = nkeys - (lt - 1) * kKT;
+#pragma unroll
+                for (int i = 0; i < LOADS; ++i) {
+                    const uint32_t at = 16u * (kThreads * i + (tid & ~63));
+                    const uint32_t r = (uint32_t)(tid + kThreads * i) / CPR, back = r < left ? 0u : r * row * 2u;
+                    dma16s(kb, koff[i] - back, (lds_ptr)(S + at));
+                    dma16s(vb, voff[i] - back, (lds_ptr)(S + sizeof(_Float16) * kKT * HD + at));
+                }
+            }
+        };
 
         // the ring: tile t in stage t % 4; tile t + 1 resident (its scores are computed during tile t), tiles
         // t + 2 and t + 3 in flight
         __syncthreads();   // the ring and the page table are free (a previous row tile's last reads are done)
         if (PTL && a.pages) {
-            const uint32_t npages = (uint32_t)((nkeys + a.page_size - 1) / a.page_size);
+            const uint32_t npages = (nkeys + a.page_size - 1) / a.page_size;
             for (uint32_t j = tid; j < npages; j += kThreads) pt[j] = a.pages[j];
             __builtin_amdgcn_s_waitcnt(0x0F70);   // vmcnt(0): the entries are in registers
             __syncthreads();                      // and in LDS for every wave
         }
-        load_tile(0, 0, nkeys);
-        if (ntiles > 1) load_tile(1, 1, nkeys);
+        load_tile();
+        if (ntiles > 1) load_tile();
         if (ntiles > 2) {
-            load_tile(2, 2, nkeys);
+            load_tile();
             __builtin_amdgcn_s_waitcnt(0x0F70 | (2 * LOADS));   // tiles 0 and 1 landed; tile 2 may fly
         } else {
             __builtin_amdgcn_s_waitcnt(0x0F70);
         }
         __syncthreads();
-        f32x16 sc = scores(0);
-        for (uint32_t t = 0; t < ntiles; ++t) {
-            const int st = t % kStages, st1 = (t + 1) % kStages, st3 = (t + 3) % kStages;
-            // tile t + 3 into the stage tile t - 1 used (every wave left it at the last barrier)
-            const bool ahead = t + 3 < ntiles;
-            if (ahead) load_tile(st3, t + 3, nkeys);
-            // the next tile's scores go to the matrix cores first; this tile's softmax runs beside them
-            f32x16 scn;
-            if (t + 1 < ntiles) scn = scores(st1);
-            const uint64_t t0 = (uint64_t)t * kKT;
-            float sv[16];
-            float mx = -INFINITY;
-            const bool diag = t0 + kKT - 1 > a.first + r0;   // some key of the tile is past some row of the wave
+
+        f32x16 sc = scores(0), scn;
+        float sv[16], mx;
+        // First half of tile t: tile t + 3's loads, tile t + 1's scores to the matrix cores, then this tile's
+        // masked scores and their row max (log2 units) beside them.
+        auto front = [&](uint32_t t) __attribute__((always_inline)) {
+            if (t + 3 < ntiles) load_tile();
+            if (t + 1 < ntiles) scn = scores((t + 1) % kStages);
+            if (t * kKT + kKT - 1 > diag_from) {   // some key of the tile is past some row of the wave
+                const int lim = (int)(mypos - t * kKT) - 4 * half;
+#pragma unroll
+                for (int r = 0; r < 16; ++r) sv[r] = 8 * (r / 4) + (r % 4) > lim ? -INFINITY : sc[r];
+            } else {
+#pragma unroll
+                for (int r = 0; r < 16; ++r) sv[r] = sc[r];
+            }
+            float x = sv[0];
+#pragma unroll
+            for (int r = 1; r < 16; ++r) x = fmaxf(x, sv[r]);
+            x = fmaxf(x, __shfl_xor(x, 32));
+            mx = x * a.scale_log2;   // the scale is positive: max and scale commute
+        };
+        // Second half: the weights 2^(s·scale − m) as fp16 P^T, their row sum, P·V, and the ring's turn.
+        auto back = [&](uint32_t t) __attribute__((always_inline)) {
+            float lsum = 0.0f;
+            f16x8 pb[2];
+            const float nm = -m;
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
-                const uint64_t key = t0 + 8 * (r / 4) + 4 * half + (r % 4);
-                float x = sc[r] * a.scale_log2;
-                if (diag && key > mypos) x = -INFINITY;
-                sv[r] = x;
-                mx = fmaxf(mx, x);
+                const float p = __builtin_amdgcn_exp2f(fmaf(sv[r], a.scale_log2, nm));
+                lsum += p;
+                pb[r / 8][r % 8] = (_Float16)p;
             }
-            mx = fmaxf(mx, __shfl_xor(mx, 32));
-            // Lazy rescale: the exponents stay against the running max m unless some row's new max passes
-            // it by more than kRescale (log2 units); then the weights are at most 2^kRescale, exact enough
-            // in fp16, and the accumulator keeps its scale. The rescale — the whole accumulator times
-            // e^(m - m') — runs only when some lane needs it (always on the first tile, rarely after).
+            l += lsum;
+            mix(t % kStages, pb);
+            if (t + 1 < ntiles) {
+                sc = scn;
+                // this wave's part of tile t + 2 landed (the next iteration computes its scores); tile t + 3's
+                // 2·LOADS loads, issued after it, may still fly — the vector-memory counter retires in order
+                if (t + 3 < ntiles) __builtin_amdgcn_s_waitcnt(0x0F70 | (2 * LOADS));
+                else __builtin_amdgcn_s_waitcnt(0x0F70);
+                __syncthreads();   // everyone's part has; everyone is done with stage st
+            }
+        };
+
+        // Lazy rescale: the exponents stay against the running max m unless some row's new max passes it by
+        // more than kRescale (log2 units); then the weights are at most 2^kRescale, exact enough in fp16,
+        // and the accumulator keeps its scale. The rescale — the whole accumulator times 2^(m − m') — runs
+        // only when some lane needs it (always on the first tile, rarely after), in place on the matrix
+        // cores' accumulator registers, so the accumulator keeps one register assignment through the loop.
+        for (uint32_t t = 0; t < ntiles; ++t) {
+            front(t);
             if (__builtin_amdgcn_ballot_w64(mx > m + kRescale)) {
                 const float mnew = fmaxf(m, mx);
                 const float corr = __builtin_amdgcn_exp2f(m - mnew);
                 l *= corr;
 #pragma unroll
-                for (int n = 0; n < DT; ++n) acc[n] *= corr;
+                for (int n = 0; n < DT; ++n)
+#pragma unroll
+                    for (int i = 0; i < 16; ++i) {
+                        float x = acc[n][i];
+                        scale_acc(x, corr);
+                        acc[n][i] = x;
+                    }
                 m = mnew;
             }
-            float lsum = 0.0f;
-            f16x8 pb[2];
-#pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                const float p = __builtin_amdgcn_exp2f(sv[r] - m);
-                lsum += p;
-                pb[r / 8][r % 8] = (_Float16)p;
-            }
-            l += lsum;
-            mix(st, pb);
-            if (t + 1 < ntiles) {
-                sc = scn;
-                // this wave's part of tile t + 2 landed (the next iteration computes its scores); tile t + 3's
-                // 2·LOADS loads, issued after it, may still fly — the vector-memory counter retires in order
-                if (ahead) __builtin_amdgcn_s_waitcnt(0x0F70 | (2 * LOADS));
-                else __builtin_amdgcn_s_waitcnt(0x0F70);
-                __syncthreads();   // everyone's part has; everyone is done with stage st
-            }
+            back(t);
         }
 
         l += __shfl_xor(l, 32);
         if (!row_ok) return;
         const float inv_l = 1.0f / l;
-        uint16_t* orow = a.o + (myrow * a.q_heads + head) * HD;
+        uint16_t* orow = a.o + ((uint64_t)myrow * a.q_heads + head) * HD;
 #pragma unroll
         for (int n = 0; n < DT; ++n)
 #pragma unroll
@@ -288,19 +351,20 @@ void causal_paged_launch(uint16_t* o, const uint16_t* q, const uint16_t* k, cons
                          uint64_t page_size, uint64_t q_heads, uint64_t kv_heads, uint64_t head_dim, uint64_t first,
                          uint64_t rows, unsigned int* over) {
     const bool ok = (head_dim == 64 || head_dim == 128 || head_dim == 256) && kv_heads > 0 && q_heads % kv_heads == 0 &&
-                    rows > 0 && first + rows < (1ull << 40) && (!pages || (page_size > 0 && page_size % kKT == 0));
+                    rows > 0 && first + rows < (1ull << 31) &&
+                    (!pages || (page_size > 0 && page_size < (1ull << 31) && page_size % kKT == 0));
     if (!ok) {
         refuse("attention_causal_paged");
         return;
     }
     CausalArgs a;
-    a.o = o; a.q = q; a.k = k; a.v = v; a.pages = pages; a.page_size = page_size;
+    a.o = o; a.q = q; a.k = k; a.v = v; a.pages = pages; a.page_size = (uint32_t)page_size;
     a.q_heads = (uint32_t)q_heads; a.kv_heads = (uint32_t)kv_heads; a.group = (uint32_t)(q_heads / kv_heads);
     a.hw = a.group % 4 == 0 ? 4 : (a.group % 2 == 0 ? 2 : 1);
     a.hblocks = a.group / a.hw;
     a.rt = 32 * (4 / a.hw);
     a.rtiles = (uint32_t)((rows + a.rt - 1) / a.rt);
-    a.first = first; a.rows = rows;
+    a.first = (uint32_t)first; a.rows = (uint32_t)rows;
     a.scale_log2 = kLog2e / sqrtf((float)head_dim);
     a.over = over;
     // pair row tiles when the causal part dominates the work (a prefix shorter than the chunk)
