@@ -50,6 +50,9 @@ def parse():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-threads", type=int, default=int(os.environ.get("BENCH_CPU_THREADS", "16")))
     ap.add_argument("--only", type=int, default=0, help="time only this config (1-5), no CPU leg")
+    ap.add_argument("--copy-probe", action="store_true",
+                    help="run a plain 1 GiB device-to-device copy 5 times and exit: the known-size kernel the "
+                         "FETCH_SIZE / WRITE_SIZE counters are scaled by")
     return ap.parse_args()
 
 
@@ -93,8 +96,8 @@ def traffic_for(kernel, workload):
     if not f.exists():
         return None
     try:
-        d = json.loads(f.read_text())
-        return d.get(f"{kernel}:{workload}")
+        d = json.loads(f.read_text()).get(f"{kernel}:{workload}")
+        return None if d is None else d["traffic_bytes"]
     except Exception:
         return None
 
@@ -189,7 +192,7 @@ def cpu_baseline(w, threads):
                 fn(qs[u], kk, vv, w.q_heads, w.kv_heads, w.head_dim, int(w.lens[u]))
                 total += time.perf_counter() - t0
             reps += 1
-            if time.perf_counter() - t_all > budget / len(routes) or reps >= 20:
+            if time.perf_counter() - t_all > budget / len(routes) or reps >= 400:
                 break
         gbs = w.io_bytes() * reps / total / 1e9
         if best is None or gbs > best[0]:
@@ -211,6 +214,15 @@ def main():
     from silvann_amd import workloads as W
     silvann_amd.lib()
     dev = torch.device("cuda:0")
+
+    if a.copy_probe:
+        src = torch.ones(1 << 29, dtype=torch.float16, device=dev)   # 1 GiB
+        dst = torch.empty_like(src)
+        for _ in range(5):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_probe_bytes": src.numel() * 2, "launches": 5}), flush=True)
+        return
 
     if a.only:
         w = W.CONFIGS[a.only](dev=dev)

@@ -136,12 +136,22 @@ uint64_t silvann_gfx950_attention_decode_paged_scratch(uint64_t q_heads, uint64_
  * 0 .. first + r; out o + r·q_heads·head_dim. One sequence (page table `pages`, `pages` NULL for a contiguous
  * cache). The fused form of `attention_causal_scores_grouped` + `attention_causal_softmax` +
  * `attention_causal_mix` (gpu.cuh:191,192,156) as the reference's `nn__attention__rows` runs them
- * (attention__abi.cuh:407-414), on fp16 MFMA with fp32 accumulation; no weights are materialised. */
+ * (attention__abi.cuh:407-414), on fp16 MFMA with fp32 accumulation; no weights are materialised.
+ * first + rows < 2^31 and page_size a multiple of 32 below 2^31; other shapes are refused (nothing launched,
+ * the refusal remembered for silvann_gfx950_launch_failed). */
 #define SILVANN_GFX950_ROW_ATTENTION_CAUSAL_PAGED 138u
 void silvann_gfx950_attention_causal_paged(uint16_t* o, const uint16_t* q, const uint16_t* k, const uint16_t* v,
                                            const uint32_t* pages, uint64_t page_size, uint64_t q_heads,
                                            uint64_t kv_heads, uint64_t head_dim, uint64_t first, uint64_t rows,
                                            unsigned int* over);
+
+/* Puts this library's rows into an nn door table: `nn_doors` is the reference's `nn__doors` (a uint32 `size`
+ * in bytes, then one function pointer a row from byte 8, gpu.cuh:93-241; entry.cuh:33-45 fills it). Every row
+ * above whose index the table's size reaches is overwritten with this library's door, as a family's
+ * override step does (amd_rocm_base/overrides/doors.cuh:20 `amd_rocm_base__override_doors`, called once
+ * from entry.cuh:72-78); rows past its size are left alone — an older table does not grow. Answers the number
+ * of rows written; 0 for a NULL table. */
+uint32_t silvann_gfx950_attention_install(void* nn_doors);
 
 /* ── library control (no reference counterpart: the reference family's launch and sys doors do this) ── */
 
@@ -149,8 +159,9 @@ void silvann_gfx950_attention_causal_paged(uint16_t* o, const uint16_t* q, const
  * reference family's choice, amd_rocm_base/nn.cuh:25-34). Thread-local, as a runner thread is a worker's. */
 void silvann_gfx950_set_stream(void* stream);
 void* silvann_gfx950_get_stream(void);
-/* Nonzero if a launch on this thread failed since the last call (the reference remembers a refused launch so
- * that the next compute_completed answers false, amd_rocm_base/nn.cuh:29-33); clears it. */
+/* Nonzero if a door on the current device refused its operands or failed to launch since the last call; clears
+ * it. Kept per device, not per thread, as the reference family keeps it (the next compute_completed on that
+ * device answers false, amd_rocm_base/sys.cuh:39-62 and amd_rocm_base/nn.cuh:29-33). */
 int silvann_gfx950_launch_failed(void);
 /* Live kernel timing: with profiling on, this thread's doors bracket their main kernels with hipEvents on
  * their stream. `kernel` is "decode_split", "decode_merge" or "causal_mfma"; read synchronises, answers the

@@ -43,6 +43,7 @@ SIGNATURES = {
     "silvann_gfx950_launch_failed": [],
     "silvann_gfx950_profile_enable": [C.c_int],
     "silvann_gfx950_profile_read": [C.c_char_p, C.POINTER(C.c_double), C.POINTER(C.c_uint64)],
+    "silvann_gfx950_attention_install": [_p],
     "silvann_gfx950_version": [],
 }
 RESTYPES = {
@@ -50,6 +51,7 @@ RESTYPES = {
     "silvann_gfx950_get_stream": _p,
     "silvann_gfx950_launch_failed": C.c_int,
     "silvann_gfx950_profile_read": C.c_int,
+    "silvann_gfx950_attention_install": C.c_uint32,
     "silvann_gfx950_version": C.c_char_p,
 }
 
@@ -64,7 +66,7 @@ _LIB = None
 def header_functions() -> list[str]:
     """Every function include/silvann_gfx950_attention.h declares."""
     text = HEADER.read_text()
-    return re.findall(r"^\s*(?:void|uint64_t|int|const char\*|void\*)\s+(silvann_gfx950_\w+)\s*\(", text, re.M)
+    return re.findall(r"^\s*(?:void|uint64_t|uint32_t|int|const char\*|void\*)\s+(silvann_gfx950_\w+)\s*\(", text, re.M)
 
 
 def lib() -> C.CDLL:

@@ -7,9 +7,11 @@
 //
 //   plan    decode_plan: each row's split count, prefix-summed, and the work counter zeroed — in the
 //           scratch's header
-//   pass 1  decode_split: exactly as many workgroups of 4 waves as the chip holds at once; each takes work
-//           items — (split of `chunk` positions of a row, kv head, head block of up to 16 query heads) — from
-//           the counter until none are left, so rows of any lengths balance over the CUs. Each wave walks
+//   pass 1  decode_split: one workgroup of 4 waves a work item — (split of `chunk` positions of a row, kv
+//           head, head block of up to 16 query heads) — flattened over the rows by the plan's prefix sums,
+//           so a short row costs only its own splits and no workgroup idles (a persistent variant that
+//           takes items from the counter instead is kept behind SILVANN_GFX950_DECODE_PERSISTENT=1; it
+//           measured slower). Each wave walks
 //           32 KB tiles of K and V (32 keys at head_dim 256, 64 at 128, 128 at 64) of the split:
 //             S^T = K · Q^T     v_mfma_f32_16x16x32_f16, keys as M, the group's query heads as N (a group of
 //                               8 fills half the columns; the other half is zero — the decode is HBM-bound,

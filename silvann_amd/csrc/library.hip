@@ -3,6 +3,7 @@
 #include <stdio.h>
 #include <string.h>
 
+#include <atomic>
 #include <vector>
 
 #include "common.hpp"
@@ -11,9 +12,17 @@
 namespace silvann {
 
 // A door runs on its caller's thread, a worker's runner thread bound to its device (reference
-// engine/src/engine/launch.cuh:51-60), so the stream and the failure flag are the thread's own.
+// engine/src/engine/launch.cuh:51-60), so the stream is the thread's own. A refused or failed launch is
+// remembered for its DEVICE, as the reference family does (amd_rocm_base/sys.cuh:39-62): the thread that
+// waits for a worker's answer is not always the thread that launched there.
 static thread_local hipStream_t tls_stream = nullptr;
-static thread_local int tls_failed = 0;
+constexpr int kDevicesSeen = 64;
+static std::atomic<int> failed[kDevicesSeen];
+
+static void mark_failed() {
+    int d = -1;
+    if (hipGetDevice(&d) == hipSuccess && d >= 0 && d < kDevicesSeen) failed[d].store(1);
+}
 
 hipStream_t stream() { return tls_stream; }
 
@@ -21,7 +30,7 @@ void check_launch(const char* what) {
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) {
         fprintf(stderr, "silvann_gfx950: launch of %s failed: %s\n", what, hipGetErrorString(e));
-        tls_failed = 1;
+        mark_failed();
     }
 }
 
@@ -62,7 +71,7 @@ void prof_end(int kernel) {
 
 void refuse(const char* what) {
     fprintf(stderr, "silvann_gfx950: %s refused its operands\n", what);
-    tls_failed = 1;
+    mark_failed();
 }
 
 }  // namespace silvann
@@ -70,9 +79,9 @@ void refuse(const char* what) {
 SILVANN_EXPORT void silvann_gfx950_set_stream(void* s) { silvann::tls_stream = (hipStream_t)s; }
 SILVANN_EXPORT void* silvann_gfx950_get_stream(void) { return (void*)silvann::tls_stream; }
 SILVANN_EXPORT int silvann_gfx950_launch_failed(void) {
-    int f = silvann::tls_failed;
-    silvann::tls_failed = 0;
-    return f;
+    int d = -1;
+    if (hipGetDevice(&d) != hipSuccess || d < 0 || d >= silvann::kDevicesSeen) return 0;
+    return silvann::failed[d].exchange(0);
 }
 static int prof_index(const char* kernel) {
     static const char* names[silvann::kProfKernels] = {"decode_split", "decode_merge", "causal_mfma"};
@@ -102,6 +111,49 @@ SILVANN_EXPORT int silvann_gfx950_profile_read(const char* kernel, double* total
     if (total_ms) *total_ms = sum;
     if (launches) *launches = n;
     return 0;
+}
+
+namespace {
+struct Row {
+    uint32_t index;
+    void* fn;
+};
+}  // namespace
+
+SILVANN_EXPORT uint32_t silvann_gfx950_attention_install(void* nn_doors) {
+    if (!nn_doors) return 0;
+    const Row rows[] = {
+        {SILVANN_GFX950_ROW_ATTENTION_SCORES, (void*)&silvann_gfx950_attention_scores},
+        {SILVANN_GFX950_ROW_ATTENTION_MIX, (void*)&silvann_gfx950_attention_mix},
+        {SILVANN_GFX950_ROW_ATTENTION_WEIGHTS, (void*)&silvann_gfx950_attention_weights},
+        {SILVANN_GFX950_ROW_ATTENTION_RESIDUAL_MIX, (void*)&silvann_gfx950_attention_residual_mix},
+        {SILVANN_GFX950_ROW_ATTENTION_MERGE, (void*)&silvann_gfx950_attention_merge},
+        {SILVANN_GFX950_ROW_ATTENTION_FINISH, (void*)&silvann_gfx950_attention_finish},
+        {SILVANN_GFX950_ROW_ATTENTION_CAUSAL_SCORES, (void*)&silvann_gfx950_attention_causal_scores},
+        {SILVANN_GFX950_ROW_ATTENTION_CAUSAL_MIX, (void*)&silvann_gfx950_attention_causal_mix},
+        {SILVANN_GFX950_ROW_ATTENTION_SCORES_GROUPED, (void*)&silvann_gfx950_attention_scores_grouped},
+        {SILVANN_GFX950_ROW_ATTENTION_SOFTMAX_ROWS, (void*)&silvann_gfx950_attention_softmax_rows},
+        {SILVANN_GFX950_ROW_ATTENTION_CAUSAL_SCORES_GROUPED, (void*)&silvann_gfx950_attention_causal_scores_grouped},
+        {SILVANN_GFX950_ROW_ATTENTION_CAUSAL_SOFTMAX, (void*)&silvann_gfx950_attention_causal_softmax},
+        {SILVANN_GFX950_ROW_ATTENTION_WEIGHTS_ROWS, (void*)&silvann_gfx950_attention_weights_rows},
+        {SILVANN_GFX950_ROW_ATTENTION_RESIDUAL_MIX_ROWS, (void*)&silvann_gfx950_attention_residual_mix_rows},
+        {SILVANN_GFX950_ROW_ATTENTION_SCORES_GROUPED_ROWS, (void*)&silvann_gfx950_attention_scores_grouped_rows},
+        {SILVANN_GFX950_ROW_ATTENTION_SOFTMAX_LENS, (void*)&silvann_gfx950_attention_softmax_lens},
+        {SILVANN_GFX950_ROW_ATTENTION_MIX_ROWS, (void*)&silvann_gfx950_attention_mix_rows},
+        {SILVANN_GFX950_ROW_ATTENTION_DECODE_PAGED, (void*)&silvann_gfx950_attention_decode_paged},
+        {SILVANN_GFX950_ROW_ATTENTION_CAUSAL_PAGED, (void*)&silvann_gfx950_attention_causal_paged},
+    };
+    uint32_t size;
+    memcpy(&size, nn_doors, sizeof size);
+    const uint64_t slots = size >= 8 ? (size - 8) / sizeof(void*) : 0;
+    void** table = (void**)((char*)nn_doors + 8);
+    uint32_t n = 0;
+    for (const Row& r : rows)
+        if (r.index < slots) {
+            table[r.index] = r.fn;
+            ++n;
+        }
+    return n;
 }
 
 SILVANN_EXPORT const char* silvann_gfx950_version(void) {

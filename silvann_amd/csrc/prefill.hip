@@ -8,18 +8,20 @@
 // multiple of 4, fewer heads over more rows), so a K/V tile in LDS serves four heads. A wave owns 32 query
 // rows of one head. Per 32-key tile:
 //   S^T = K · Q^T      v_mfma_f32_32x32x16_f16: keys as M, the wave's rows as N, head dims as K; Q^T stays
-//                      in registers, K comes from LDS; four independent accumulator chains
+//                      in registers, K comes from LDS; one accumulator chain
 //   online softmax     a lane owns one row (its column of S^T, 16 keys); the row's other 16 keys are in lane
 //                      l ^ 32, one exchange away; exponents in base 2 with the scale folded in
 //   O^T += V^T · P^T   the same MFMA with keys as K: P^T is the S^T registers narrowed to fp16; V^T is read
 //                      from the row-major tile with the transposing LDS read (ds_read_b64_tr_b16), two a
 //                      k-step
-// K and V tiles move HBM → LDS directly (16 bytes a lane) through a ring of four stages: tile t + 1 is
-// resident and tiles t + 2 and t + 3 are in flight while tile t computes, one barrier a tile. Tile t + 1's scores are issued to the matrix
-// cores before tile t's softmax, so the exponentials run while the MFMAs do. Rows are XOR-swizzled in 16-byte chunks so both operand reads are
-// free of bank conflicts. Causal: keys past a row's position are masked in the diagonal tiles; tiles past
-// the workgroup's last row are never loaded. With a short prefix, a workgroup takes row tiles i and N-1-i,
-// so every workgroup has the same work.
+// K and V tiles move HBM → LDS directly (16 bytes a lane, from a scalar base plus a 32-bit lane offset)
+// through a ring of four stages: tile t + 1 is resident and tiles t + 2 and t + 3 are in flight while tile t
+// computes, one barrier a tile. Tile t + 1's scores are issued to the matrix cores before tile t's softmax,
+// so the exponentials run while the MFMAs do. Rows are XOR-swizzled in 16-byte chunks so both operand reads
+// are free of bank conflicts. Causal: keys past a row's position are masked in the diagonal tiles only;
+// tiles past the workgroup's last row are never loaded. With a short prefix, a workgroup takes row tiles i
+// and N-1-i, so every workgroup has the same work. Positions are 32-bit (first + rows < 2^31); a tile's
+// page comes from a cursor that advances a tile a load, so the loop has no 64-bit division.
 #include <math.h>
 #include <stdio.h>
 

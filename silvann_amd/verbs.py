@@ -181,7 +181,7 @@ def causal_paged(q, k, v, pages, out, q_heads, kv_heads, head_dim, first, rows, 
             or head_dim not in (64, 128, 256)):
         raise Fault(FAULT_BOUNDS)
     qw, kvw, to = q_heads * head_dim, kv_heads * head_dim, first + rows
-    if not _fits(rows * qw, room(q)) or not _fits(rows * qw, room(out)):
+    if to >= 1 << 31 or not _fits(rows * qw, room(q)) or not _fits(rows * qw, room(out)):
         raise Fault(FAULT_BOUNDS)
     if pages is None:
         if not _fits(to * kvw, room(k)) or not _fits(to * kvw, room(v)):

@@ -15,7 +15,8 @@ from tests.gpu_util import t
 
 pytestmark = pytest.mark.gpu
 
-SHAPES = [(16, 2, 256, 333), (8, 8, 64, 65), (32, 4, 128, 1000), (64, 1, 128, 100), (6, 2, 72, 50)]
+SHAPES = [(16, 2, 256, 333), (8, 8, 64, 65), (32, 4, 128, 1000), (64, 1, 128, 100), (6, 2, 72, 50),
+          (6, 3, 9, 41)]   # an odd head_dim takes the dots' per-element arm (kernels.cuh:986-990)
 
 
 def close(got, want, atol, rtol=0.0):
@@ -120,6 +121,42 @@ def test_grouped_and_softmax_rows(dev, oracle, qh, kvh, hd, L):
     close(p.cpu().numpy(), wp, 1e-4, 2e-5)
     doors.attention_softmax_rows(p, qh, L)
     close(p.cpu().numpy(), oracle.softmax_rows(wp, qh, L), 1e-5)
+
+
+def test_unaligned_query_and_odd_head_dim_grouped(dev, oracle):
+    """A query 2 bytes past a 4-byte boundary, and an odd head_dim: the element-wise arm of the dots."""
+    for qh, kvh, hd, L in ((8, 2, 64, 50), (6, 3, 9, 41)):
+        buf, k = inputs(600 + hd, (qh * hd + 1,), (L * kvh * hd,))
+        qd = t(buf, dev)
+        p = dev_zeros(qh * L, torch.float32, dev)
+        print(f"case: grouped unaligned q qh{qh} kvh{kvh} hd{hd} L{L}", flush=True)
+        doors.attention_scores_grouped(p, qd.data_ptr() + 2, t(k, dev), qh, kvh, hd, L)
+        close(p.cpu().numpy(), oracle.scores_grouped(buf[1:], k, qh, kvh, hd, L), 1e-4, 2e-5)
+
+
+def test_refused_shape_launches_nothing(dev):
+    """A door given a shape it does not take launches nothing, leaves its output alone and reports the
+    refusal through silvann_gfx950_launch_failed (then clears it)."""
+    doors.launch_failed()   # clears what an earlier test may have left
+    o = torch.full((16 * 96,), 7.0, dtype=torch.float16, device=dev)
+    q = torch.zeros(16 * 96, dtype=torch.float16, device=dev)
+    kv = torch.zeros(64 * 2 * 96, dtype=torch.float16, device=dev)
+    lens = torch.tensor([64], dtype=torch.int32, device=dev)
+    scratch = torch.zeros(1 << 20, dtype=torch.uint8, device=dev)
+    over = dev_zeros(1, torch.int32, dev)
+    doors.attention_decode_paged(o, q, kv, kv, None, 0, 0, 0, lens, 16, 2, 96, 64, 1, scratch, over)   # head_dim 96
+    torch.cuda.synchronize()
+    assert doors.launch_failed() == 1
+    assert doors.launch_failed() == 0
+    assert torch.all(o == 7.0)
+    # refused on another thread, read on this one: the flag is the device's (amd_rocm_base/sys.cuh:39-62)
+    import threading
+    th = threading.Thread(target=lambda: doors.attention_causal_paged(o, q, kv, kv, None, 0, 16, 2, 96, 0, 64, over))
+    th.start()
+    th.join()
+    torch.cuda.synchronize()
+    assert doors.launch_failed() == 1
+    assert torch.all(o == 7.0) and int(over.item()) == 0
 
 
 def test_lens_rows(dev, oracle):
