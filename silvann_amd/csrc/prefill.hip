@@ -299,8 +299,7 @@ __global__ __launch_bounds__(kThreads) void causal_mfma(CausalArgs a) {
         // and the accumulator keeps its scale. The rescale — the whole accumulator times 2^(m − m') — runs
         // only when some lane needs it (always on the first tile, rarely after), in place on the matrix
         // cores' accumulator registers, so the accumulator keeps one register assignment through the loop.
-        for (uint32_t t = 0; t < ntiles; ++t) {
-            front(t);
+        auto rescale = [&]() __attribute__((always_inline)) {
             if (__builtin_amdgcn_ballot_w64(mx > m + kRescale)) {
                 const float mnew = fmaxf(m, mx);
                 const float corr = __builtin_amdgcn_exp2f(m - mnew);
@@ -315,6 +314,94 @@ __global__ __launch_bounds__(kThreads) void causal_mfma(CausalArgs a) {
                     }
                 m = mnew;
             }
+        };
+
+        // Steady state: tiles wholly below the wave's diagonal whose load three tiles ahead is a full tile.
+        // One branch-free block a tile, in the order the matrix cores want it: tile t + 1's scores (16
+        // MFMAs) with tile t's exponentials, sums and fp16 packing between them, then tile t's P·V (16
+        // MFMAs) with tile t + 1's row max between them; the instruction groups are pinned so each MFMA has
+        // vector work to hide behind and its LDS operand was read a few MFMAs earlier.
+        // Built for head_dim 256 only (the other widths keep the generic loop). steady_end is wave-uniform
+        // by construction (the wave's rows); readfirstlane says so to the compiler, which otherwise lowers
+        // this loop and the tail after it as divergent, with the tile cursor in vector registers.
+        uint32_t t = 0;
+        if constexpr (HD == 256) {
+        const uint32_t below = (diag_from + 1) / kKT;   // tiles t with 32·t + 31 <= diag_from
+        const uint32_t steady_end = __builtin_amdgcn_readfirstlane(min(ntiles > 4 ? ntiles - 4 : 0u, below));
+        if (steady_end > 0) {
+            float x = sc[0];
+#pragma unroll
+            for (int r = 1; r < 16; ++r) x = fmaxf(x, sc[r]);
+            x = fmaxf(x, __shfl_xor(x, 32));
+            mx = x * a.scale_log2;
+        }
+        for (; t < steady_end; ++t) {
+            rescale();
+            load_tile();
+            const char* SK = (const char*)ring[(t + 1) % kStages].k;
+            const char* SV = (const char*)ring[t % kStages].v;
+            auto kread_at = [&](int kk) __attribute__((always_inline)) {
+                return *(const f16x8*)(SK + kread[kk % 8] + 256 * (kk / 8));
+            };
+            auto vread_at = [&](int i) __attribute__((always_inline)) {   // MFMA i: k-step i / DT, dim tile i % DT
+                const int s2 = i / DT, n = i % DT;
+                const s16x4 x0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                    (__attribute__((address_space(3))) s16x4*)(SV + vread[n % 4] + 256 * (n / 4) + (16 * s2) * RB));
+                const s16x4 x1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                    (__attribute__((address_space(3))) s16x4*)(SV + vread[n % 4] + 256 * (n / 4) + (16 * s2 + 8) * RB));
+                return __builtin_bit_cast(f16x8, __builtin_shufflevector(x0, x1, 0, 1, 2, 3, 4, 5, 6, 7));
+            };
+            constexpr int KA = 4, VA = 2;   // operand reads ahead of their MFMA
+            f16x8 kb[KA + 1], vb[VA + 2];
+            f32x16 c = (f32x16)0.0f;
+            float lsum = 0.0f;
+            f16x8 pb[2];
+            const float nm = -m;
+#pragma unroll
+            for (int kk = 0; kk < KA && kk < KSTEPS; ++kk) kb[kk] = kread_at(kk);
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int kk = 0; kk < KSTEPS; ++kk) {
+                c = __builtin_amdgcn_mfma_f32_32x32x16_f16(kb[kk % (KA + 1)], qb[kk], c, 0, 0, 0);
+                if (kk + KA < KSTEPS) kb[(kk + KA) % (KA + 1)] = kread_at(kk + KA);
+                if (kk + KA == KSTEPS) vb[0] = vread_at(0);
+                if (kk + KA == KSTEPS + 1) vb[1] = vread_at(1);
+                // the weights of tile t, spread over the MFMAs (one each when KSTEPS is 16)
+#pragma unroll
+                for (int r = kk * 16 / KSTEPS; r < (kk + 1) * 16 / KSTEPS; ++r) {
+                    const float p = __builtin_amdgcn_exp2f(fmaf(sc[r], a.scale_log2, nm));
+                    lsum += p;
+                    pb[r / 8][r % 8] = (_Float16)p;
+                }
+                __builtin_amdgcn_sched_barrier(0);
+            }
+            if (KSTEPS < KA + 1) { vb[0] = vread_at(0); vb[1] = vread_at(1); }
+            l += lsum;
+            float x = 0.0f;
+#pragma unroll
+            for (int i = 0; i < 2 * DT; ++i) {
+                acc[i % DT] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vb[i % (VA + 2)], pb[i / DT], acc[i % DT], 0, 0, 0);
+                if (i + VA < 2 * DT) vb[(i + VA) % (VA + 2)] = vread_at(i + VA);
+                // tile t + 1's row max, once its scores are out of the matrix cores
+                if (i == 2) x = fmaxf(c[0], c[1]);
+                if (i >= 3 && i < 10) x = fmaxf(x, fmaxf(c[2 * (i - 2)], c[2 * (i - 2) + 1]));
+                __builtin_amdgcn_sched_barrier(0);
+            }
+            if (2 * DT < 11) {
+                x = c[0];
+#pragma unroll
+                for (int r = 1; r < 16; ++r) x = fmaxf(x, c[r]);
+            }
+            sc = c;
+            x = fmaxf(x, __shfl_xor(x, 32));
+            mx = x * a.scale_log2;
+            __builtin_amdgcn_s_waitcnt(0x0F70 | (2 * LOADS));   // tile t + 2 landed; tile t + 3 may fly
+            __syncthreads();
+        }
+        }
+        for (; t < ntiles; ++t) {
+            front(t);
+            rescale();
             back(t);
         }
 
