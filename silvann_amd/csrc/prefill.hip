@@ -24,6 +24,10 @@
 // page comes from a cursor that advances a tile a load, so the loop has no 64-bit division.
 #include <math.h>
 #include <stdio.h>
+#include <stdlib.h>
+#include <string.h>
+
+#include <type_traits>
 
 #include "common.hpp"
 #include "../../include/silvann_gfx950_attention.h"
@@ -77,11 +81,26 @@ constexpr float kRescale = 8.0f;
 
 typedef __attribute__((address_space(3))) void* lds_ptr;
 
+// s_waitcnt's immediate for "vector-memory count <= n" alone (n < 64): the count's low four bits sit in
+// bits 3:0 and its high two in bits 15:14; expcnt and lgkmcnt are left at their maxima (no wait).
+constexpr int vmcnt_only(int n) { return 0x0F70 | (n & 0xF) | ((n >> 4) << 14); }
+
 // A uniform 32-bit load through the scalar cache (a read; the page table is never written by the kernel).
 __device__ __forceinline__ uint32_t scalar_load(const uint32_t* p) {
     uint32_t x;
     asm volatile("s_load_dword %0, %1, 0x0\n\ts_waitcnt lgkmcnt(0)" : "=s"(x) : "s"(p) : "memory");
     return x;
+}
+
+// dma16s with one wait state after the load, so the next write of M0 (the next load's LDS address) is never
+// the very next instruction: the spacing the compiler's own schedules keep for this instruction.
+__device__ __forceinline__ void dma16s_gap(const void* base, uint32_t off, lds_ptr lds) {
+    const uint32_t m0 = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)lds);
+    const uint64_t b = (uint64_t)(uintptr_t)base;
+    const uint32_t lo = (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)b);
+    const uint32_t hi = (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)(b >> 32));
+    const uint64_t sb = ((uint64_t)hi << 32) | (uint64_t)lo;
+    asm volatile("global_load_lds_dwordx4 %0, %1\n\ts_nop 0" : : "v"(off), "s"(sb), "{m0}"(m0) : "memory");
 }
 
 // x *= c for an accumulator element held in an accumulation register, in place.
@@ -434,7 +453,349 @@ __global__ __launch_bounds__(kThreads) void causal_mfma(CausalArgs a) {
     if (hit) *a.over = kFaultOverflow;
 }
 
+// ── causal_pipe: the head_dim-256 kernel, software-pipelined two tiles deep ────────────────────────────
+//
+// The same workgroup shape, operand layouts, swizzles and online softmax as causal_mfma, scheduled so that
+// no step of a tile waits on the step before it. Iteration t of a wave:
+//   matrix cores   S(t + 2) = K(t + 2) · Q^T (16 MFMAs, one accumulator chain) alternating one for one
+//                  with O^T += V(t)^T · P(t)^T (16 MFMAs over the 8 accumulator tiles), each operand read
+//                  from LDS two MFMAs ahead into rotating registers
+//   vector unit    tile t + 1's softmax between them: its row max (the partner half of the row by one
+//                  v_permlane32_swap), the lazy max update, and its weights 2^(s·scale − m) narrowed to
+//                  fp16 as P(t + 1)
+//   memory         K(t + 5) and V(t + 3) straight into LDS, so every tile has two iterations to land
+// The max update only decides: a changed max rescales l at once and the accumulator at the top of the next
+// iteration, after P(t)·V has gone in at the old scale. K and V have rings of their own, four stages each;
+// tile j lives in stage j % 4 of each. While K(t + 5) exists every iteration issues the same loads and one
+// vmcnt count serves them all; the last iterations load what exists and wait for everything. Iterations
+// whose tile t + 1 is diagonal or that are among the last five take a general path with the mask and the
+// bounds.
+template <int HD, bool PAIRED, bool PTL>
+__global__ __launch_bounds__(kThreads) void causal_pipe(CausalArgs a) {
+    constexpr int CPR = HD / 8;
+    constexpr int KSTEPS = HD / 16;   // S MFMAs a tile; also the P·V MFMAs a tile (2 k-steps × HD / 32)
+    constexpr int DT = HD / 32;
+    constexpr int LOADS = kKT * CPR / kThreads;
+    constexpr uint32_t RB = 2 * HD;
+    constexpr int NS = 4;                              // stages of each ring
+    constexpr int GROUP = 2 * LOADS;                   // direct loads a thread issues an iteration
+    static_assert(2 * DT == KSTEPS, "one P·V MFMA for each S MFMA");
+    __shared__ __attribute__((aligned(16))) _Float16 kring[NS][kKT * HD];
+    __shared__ __attribute__((aligned(16))) _Float16 vring[NS][kKT * HD];
+    __shared__ uint32_t pt[PTL ? kPagesInLds : 1];
+
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const int col = lane & 31, half = lane >> 5;
+    const uint32_t g = blockIdx.y / a.hblocks, hb = blockIdx.y % a.hblocks;
+    const uint32_t head = g * a.group + hb * a.hw + (w % a.hw);
+    const uint32_t row = a.kv_heads * HD;
+    bool hit = false;
+
+    uint32_t koff[LOADS], voff[LOADS];
+#pragma unroll
+    for (int i = 0; i < LOADS; ++i) {
+        const int s = tid + kThreads * i, r = s / CPR, pc = s % CPR;
+        koff[i] = (uint32_t)r * row * 2u + 16u * kslot<CPR>(r, pc);
+        voff[i] = (uint32_t)r * row * 2u + 16u * vslot<CPR>(r, pc);
+    }
+    constexpr int KR = KSTEPS < 8 ? KSTEPS : 8, VR = DT < 4 ? DT : 4;
+    uint32_t kread[KR], vread[VR];
+    {
+        const int blk = lane >> 4, li = lane & 15, jj = li >> 2, rr = li & 3, key = 4 * half + jj;
+#pragma unroll
+        for (int kk = 0; kk < KR; ++kk) kread[kk] = col * RB + 16u * kslot<CPR>(col, 2 * kk + half);
+#pragma unroll
+        for (int n = 0; n < VR; ++n) {
+            const int d0 = 32 * n + 16 * (blk & 1) + 4 * rr;
+            vread[n] = key * RB + 16u * vslot<CPR>(key, d0 >> 3) + 2u * (d0 & 7);
+        }
+    }
+
+    f32x16 acc[DT];
+    f16x8 qb[KSTEPS];
+
+    // S^T operand k of the tile in K stage `ks`; V^T operand i (k-step i / DT, dim tile i % DT) of V stage `vs`
+    auto kop = [&](int ks, int kk) __attribute__((always_inline)) {
+        return *(const f16x8*)((const char*)kring[ks] + kread[kk % 8] + 256 * (kk / 8));
+    };
+    auto vop = [&](int vs, int i) __attribute__((always_inline)) {
+        const char* S = (const char*)vring[vs];
+        const int s2 = i / DT, n = i % DT;
+        const s16x4 x0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+            (__attribute__((address_space(3))) s16x4*)(S + vread[n % 4] + 256 * (n / 4) + (16 * s2) * RB));
+        const s16x4 x1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+            (__attribute__((address_space(3))) s16x4*)(S + vread[n % 4] + 256 * (n / 4) + (16 * s2 + 8) * RB));
+        return __builtin_bit_cast(f16x8, __builtin_shufflevector(x0, x1, 0, 1, 2, 3, 4, 5, 6, 7));
+    };
+    // the larger of a lane's value and its row partner's (lane ^ 32)
+    auto pair_max = [](float x) __attribute__((always_inline)) {
+        const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+        return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+    };
+
+    auto process = [&](uint32_t rtile) __attribute__((always_inline)) {
+        const uint32_t wg_r0 = rtile * a.rt;
+        const uint32_t r0 = wg_r0 + (w / a.hw) * 32;
+        const uint32_t wg_rlast = min(a.rows, wg_r0 + a.rt) - 1;
+        const uint32_t nkeys = a.first + wg_rlast + 1;
+        const uint32_t ntiles = (nkeys + kKT - 1) / kKT;
+        const uint32_t myrow = r0 + col;
+        const bool row_ok = myrow < a.rows;
+        {
+            const uint16_t* qr = a.q + ((uint64_t)(row_ok ? myrow : 0) * a.q_heads + head) * HD;
+#pragma unroll
+            for (int kk = 0; kk < KSTEPS; ++kk) qb[kk] = *(const f16x8*)(qr + 16 * kk + 8 * half);
+        }
+        const uint32_t mypos = a.first + (row_ok ? myrow : 0);
+        const uint32_t diag_from = a.first + r0;
+#pragma unroll
+        for (int n = 0; n < DT; ++n) acc[n] = (f32x16)0.0f;
+        float m = -INFINITY, l = 0.0f, corr = 1.0f;
+        uint64_t rescale = 0;   // lanes whose max moved: the accumulator waits for its factor `corr`
+
+        __syncthreads();   // both rings and the page table are free
+        if (PTL && a.pages) {
+            const uint32_t npages = (nkeys + a.page_size - 1) / a.page_size;
+            for (uint32_t j = tid; j < npages; j += kThreads) pt[j] = a.pages[j];
+            __builtin_amdgcn_s_waitcnt(0x0F70);
+            __syncthreads();
+        }
+
+        // Load cursors, one a plane: the next tile to load, its page and the offset in it (page_size is a
+        // multiple of the tile).
+        struct Cursor { uint32_t j, lj, loff, page; };
+        auto lookup = [&](uint32_t lj) __attribute__((always_inline)) -> uint32_t {
+            if constexpr (PTL) return __builtin_amdgcn_readfirstlane(pt[lj]);
+            else return scalar_load(a.pages + lj);
+        };
+        Cursor ck{0, 0, 0, 0}, cv{0, 0, 0, 0};
+        if (a.pages) ck.page = cv.page = lookup(0);
+        // Tile c.j of K (ISK) or V into its stage, 16 bytes a lane, LOADS a thread; in the last (partial)
+        // tile keys past the cache bring the tile's key 0 (masked). The cursor then moves to the next tile.
+        // Only tiles that exist are loaded, so no two loads in flight ever target the same bytes.
+        auto issue = [&](auto isk, Cursor& c) __attribute__((always_inline)) {
+            constexpr bool ISK = decltype(isk)::value;
+            uint64_t base = a.pages ? ((uint64_t)c.page * a.page_size + c.loff) * row : (uint64_t)c.j * kKT * row;
+            base += (uint64_t)g * HD;
+            const uint16_t* pb = (ISK ? a.k : a.v) + base;
+            const uint32_t* off = ISK ? koff : voff;
+            char* S = ISK ? (char*)kring[c.j % NS] : (char*)vring[c.j % NS];
+            if ((c.j + 1) * kKT <= nkeys) {
+#pragma unroll
+                for (int i = 0; i < LOADS; ++i) dma16s_gap(pb, off[i], (lds_ptr)(S + 16u * (kThreads * i + (tid & ~63))));
+            } else {
+                const uint32_t left = nkeys - c.j * kKT;
+#pragma unroll
+                for (int i = 0; i < LOADS; ++i) {
+                    const uint32_t r = (uint32_t)(tid + kThreads * i) / CPR, back = r < left ? 0u : r * row * 2u;
+                    dma16s_gap(pb, off[i] - back, (lds_ptr)(S + 16u * (kThreads * i + (tid & ~63))));
+                }
+            }
+            ++c.j;
+            if (a.pages && c.j < ntiles) {
+                c.loff += kKT;
+                if (c.loff == a.page_size) {
+                    c.loff = 0;
+                    ++c.lj;
+                    c.page = lookup(c.lj);
+                }
+            }
+        };
+        using KT = std::integral_constant<bool, true>;
+        using VT = std::integral_constant<bool, false>;
+        auto issue_k = [&]() __attribute__((always_inline)) { if (ck.j < ntiles) issue(KT{}, ck); };
+        auto issue_v = [&]() __attribute__((always_inline)) { if (cv.j < ntiles) issue(VT{}, cv); };
+
+        // S^T of the K tile in stage ks, one accumulator chain
+        auto scores = [&](int ks) __attribute__((always_inline)) -> f32x16 {
+            f32x16 c = (f32x16)0.0f;
+#pragma unroll
+            for (int kk = 0; kk < KSTEPS; ++kk) c = __builtin_amdgcn_mfma_f32_32x32x16_f16(kop(ks, kk), qb[kk], c, 0, 0, 0);
+            return c;
+        };
+        // Softmax of raw scores s (tile j): the lazy max update, the weights as fp16 P^T, l at the new scale.
+        // MASK: keys past the row's position are -inf (a diagonal tile).
+        auto softmax = [&](f32x16 s, uint32_t j, bool mask, f16x8* pbn) __attribute__((always_inline)) {
+            float sv[16];
+            if (mask) {
+                const int lim = (int)(mypos - j * kKT) - 4 * half;
+#pragma unroll
+                for (int r = 0; r < 16; ++r) sv[r] = 8 * (r / 4) + (r % 4) > lim ? -INFINITY : s[r];
+            } else {
+#pragma unroll
+                for (int r = 0; r < 16; ++r) sv[r] = s[r];
+            }
+            float x = sv[0];
+#pragma unroll
+            for (int r = 1; r < 16; ++r) x = fmaxf(x, sv[r]);
+            const float mx = pair_max(x) * a.scale_log2;
+            const float mnew = mx > m + kRescale ? fmaxf(m, mx) : m;
+            const float c = mnew == m ? 1.0f : __builtin_amdgcn_exp2f(m - mnew);
+            rescale = __builtin_amdgcn_ballot_w64(mnew != m);
+            corr = c;
+            m = mnew;
+            float lsum = 0.0f;
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const float p = __builtin_amdgcn_exp2f(fmaf(sv[r], a.scale_log2, -mnew));
+                lsum += p;
+                pbn[r / 8][r % 8] = (_Float16)p;
+            }
+            l = fmaf(l, c, lsum);
+        };
+        auto apply_rescale = [&]() __attribute__((always_inline)) {
+            if (rescale) {
+#pragma unroll
+                for (int n = 0; n < DT; ++n)
+#pragma unroll
+                    for (int i = 0; i < 16; ++i) {
+                        float x = acc[n][i];
+                        scale_acc(x, corr);
+                        acc[n][i] = x;
+                    }
+                rescale = 0;
+            }
+        };
+
+        // Prologue. K 0..3, V 0 and 1 go out first; once K 0 and K 1 have given S(0) and S(1) (and P(0)),
+        // K 4 and V 2 follow — K 4's stage is K 0's. Then iteration t issues K(t + 5) and V(t + 3), each
+        // into a stage whose tile every wave has finished with (the barrier closing iteration t - 1).
+        const bool full = ntiles >= 6;   // every prologue and steady group exists: exact vmcnt counts
+        issue_k(); issue_k(); issue_k(); issue_v();
+        issue_k(); issue_v();
+        if (full) __builtin_amdgcn_s_waitcnt(vmcnt_only(2 * LOADS));   // K 0..2 and V 0 landed; K 3, V 1 fly
+        else __builtin_amdgcn_s_waitcnt(vmcnt_only(0));
+        __syncthreads();
+        f32x16 sc0 = scores(0);
+        f32x16 sc = ntiles > 1 ? scores(1) : sc0;
+        f16x8 pb[2];
+        softmax(sc0, 0, kKT - 1 > diag_from, pb);
+        __syncthreads();   // K 0 is read by every wave
+        issue_k(); issue_v();
+
+        // steady: tile t + 1 wholly below the wave's diagonal and S(t + 2) inside the sequence
+        // steady: K(t + 5) exists (so S(t + 2) does) and tile t + 1 lies wholly below the wave's diagonal
+        const uint32_t below = (diag_from + 1) / kKT;   // tiles j with 32·j + 31 <= diag_from
+        const uint32_t steady_end = __builtin_amdgcn_readfirstlane(
+            min(ntiles > 5 ? ntiles - 5 : 0u, below > 1 ? below - 1 : 0u));
+        uint32_t t = 0;
+        for (; t < steady_end; ++t) {
+            apply_rescale();
+            issue_k();
+            issue_v();
+            const int ks = (t + 2) % NS, vs = t % NS;
+            f32x16 c = (f32x16)0.0f;
+            f16x8 pbn[2];
+            f16x8 kb[3], vb[3];
+            kb[0] = kop(ks, 0);
+            vb[0] = vop(vs, 0);
+            kb[1] = kop(ks, 1);
+            vb[1] = vop(vs, 1);
+            // tile t + 1's softmax, spread over the 16 MFMA pairs: the max over 4 of them, the update at the
+            // fifth, the weights over the rest
+            float x = 0.0f, mnew = 0.0f, cf = 1.0f, lsum = 0.0f;
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int k = 0; k < KSTEPS; ++k) {
+                c = __builtin_amdgcn_mfma_f32_32x32x16_f16(kb[k % 3], qb[k], c, 0, 0, 0);
+                if (k + 2 < KSTEPS) kb[(k + 2) % 3] = kop(ks, k + 2);
+                acc[k % DT] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vb[k % 3], pb[k / DT], acc[k % DT], 0, 0, 0);
+                if (k + 2 < KSTEPS) vb[(k + 2) % 3] = vop(vs, k + 2);
+                constexpr int MAXS = KSTEPS / 4 > 0 ? KSTEPS / 4 : 1;   // steps the max takes
+                if (k < MAXS) {
+#pragma unroll
+                    for (int r = k * 16 / MAXS; r < (k + 1) * 16 / MAXS; ++r) x = r == 0 ? sc[0] : fmaxf(x, sc[r]);
+                }
+                if (k == MAXS) {
+                    const float mx = pair_max(x) * a.scale_log2;
+                    mnew = mx > m + kRescale ? fmaxf(m, mx) : m;
+                    cf = mnew == m ? 1.0f : __builtin_amdgcn_exp2f(m - mnew);
+                    rescale = __builtin_amdgcn_ballot_w64(mnew != m);
+                }
+                if (k > MAXS) {
+                    constexpr int SPAN = KSTEPS - 1 - MAXS;   // steps left for the 16 weights
+                    const int e = k - MAXS - 1;
+#pragma unroll
+                    for (int r = e * 16 / SPAN; r < (e + 1) * 16 / SPAN; ++r) {
+                        const float p = __builtin_amdgcn_exp2f(fmaf(sc[r], a.scale_log2, -mnew));
+                        lsum += p;
+                        pbn[r / 8][r % 8] = (_Float16)p;
+                    }
+                }
+                __builtin_amdgcn_sched_barrier(0);
+            }
+            corr = cf;
+            m = mnew;
+            l = fmaf(l, cf, lsum);
+            pb[0] = pbn[0];
+            pb[1] = pbn[1];
+            sc = c;
+            __builtin_amdgcn_s_waitcnt(vmcnt_only(2 * GROUP));   // K(t + 3), V(t + 1) landed
+            __syncthreads();
+        }
+        // the last iterations: diagonal tiles masked, no scores past the sequence
+        for (; t < ntiles; ++t) {
+            apply_rescale();
+            issue_k();
+            issue_v();
+            f32x16 c = sc;
+            if (t + 2 < ntiles) c = scores((t + 2) % NS);
+            {
+                const int vs = t % NS;
+#pragma unroll
+                for (int i = 0; i < KSTEPS; ++i)
+                    acc[i % DT] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vop(vs, i), pb[i / DT], acc[i % DT], 0, 0, 0);
+            }
+            if (t + 1 < ntiles) {
+                f16x8 pbn[2];
+                softmax(sc, t + 1, (t + 1) * kKT + kKT - 1 > diag_from, pbn);
+                pb[0] = pbn[0];
+                pb[1] = pbn[1];
+            }
+            sc = c;
+            __builtin_amdgcn_s_waitcnt(vmcnt_only(0));   // groups shrink at the end: wait for all
+            __syncthreads();
+        }
+
+        l += __shfl_xor(l, 32);
+        if (!row_ok) return;
+        const float inv_l = 1.0f / l;
+        uint16_t* orow = a.o + ((uint64_t)myrow * a.q_heads + head) * HD;
+#pragma unroll
+        for (int n = 0; n < DT; ++n)
+#pragma unroll
+            for (int qd = 0; qd < 4; ++qd) {
+                uint16_t hv[4];
+#pragma unroll
+                for (int i = 0; i < 4; ++i) hv[i] = to_half(acc[n][4 * qd + i] * inv_l, hit);
+                const uint64_t packed = (uint64_t)hv[0] | ((uint64_t)hv[1] << 16) | ((uint64_t)hv[2] << 32) |
+                                        ((uint64_t)hv[3] << 48);
+                *(uint64_t*)(orow + 32 * n + 8 * qd + 4 * half) = packed;
+            }
+    };
+
+    if (PAIRED) {
+        const uint32_t heavy = a.rtiles - 1 - blockIdx.x, light = blockIdx.x;
+        process(heavy);
+        if (light < heavy) process(light);
+    } else {
+        process(a.rtiles - 1 - blockIdx.x);
+    }
+    if (hit) *a.over = kFaultOverflow;
+}
+
 }  // namespace
+
+// Which head_dim-256 kernel runs: causal_mfma (the default) or causal_pipe, chosen once a process by
+// SILVANN_GFX950_PREFILL=pipe. causal_pipe has been checked against the oracle in the CPU emulation of the
+// kernels (tests/emu) and has not yet run on a GPU, so it is not the default.
+static bool prefill_pipe() {
+    static const bool on = [] {
+        const char* e = getenv("SILVANN_GFX950_PREFILL");
+        return e && strcmp(e, "pipe") == 0;
+    }();
+    return on;
+}
 
 void causal_paged_launch(uint16_t* o, const uint16_t* q, const uint16_t* k, const uint16_t* v, const uint32_t* pages,
                          uint64_t page_size, uint64_t q_heads, uint64_t kv_heads, uint64_t head_dim, uint64_t first,
@@ -473,7 +834,19 @@ void causal_paged_launch(uint16_t* o, const uint16_t* q, const uint16_t* k, cons
     switch (head_dim) {
         case 64: SILVANN_CAUSAL(64) break;
         case 128: SILVANN_CAUSAL(128) break;
-        default: SILVANN_CAUSAL(256) break;
+        default:
+            if (prefill_pipe()) {
+                if (paired) {
+                    if (ptl) causal_pipe<256, true, true><<<grid, kThreads, 0, st>>>(a);
+                    else causal_pipe<256, true, false><<<grid, kThreads, 0, st>>>(a);
+                } else {
+                    if (ptl) causal_pipe<256, false, true><<<grid, kThreads, 0, st>>>(a);
+                    else causal_pipe<256, false, false><<<grid, kThreads, 0, st>>>(a);
+                }
+            } else {
+                SILVANN_CAUSAL(256)
+            }
+            break;
     }
 #undef SILVANN_CAUSAL
     prof_end(kProfCausal);
