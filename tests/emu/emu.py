@@ -1,0 +1,94 @@
+"""TEST INFRASTRUCTURE: build the CPU emulation of this library's kernels and run one call of an entry point.
+
+`build()` turns silvann_amd/csrc/{prefill,decode}.hip into host C++ (gen.py), compiles them with the
+harness against emu_rt.hpp into tests/emu/_build/emu (rebuilt when any source changes), and returns its
+path. `run_causal(w)` / `run_decode(w)` run a workload from silvann_amd.workloads through the library's own
+C entry point in the emulation and return the fp16 answer and the fault word.
+"""
+from __future__ import annotations
+
+import concurrent.futures as cf
+import hashlib
+import os
+import shutil
+import subprocess
+import tempfile
+from pathlib import Path
+
+import numpy as np
+
+HERE = Path(__file__).resolve().parent
+BUILD = HERE / "_build"
+SOURCES = ["prefill.hip", "decode.hip"]
+CXX_CANDIDATES = ["/opt/rocm/llvm/bin/clang++", "/opt/rocm/lib/llvm/bin/clang++", shutil.which("clang++") or ""]
+FLAGS = ["-std=c++20", "-O1", "-g", "-fno-omit-frame-pointer", "-rdynamic", "-w", "-pthread"]
+
+
+def compiler() -> str | None:
+    for c in CXX_CANDIDATES:
+        if c and Path(c).exists():
+            return c
+    return None
+
+
+def _digest() -> str:
+    from . import gen  # noqa: F401  (the transform is part of the key)
+    h = hashlib.sha256()
+    for f in [*(gen.CSRC / s for s in SOURCES), gen.CSRC / "common.hpp", HERE / "emu_rt.hpp", HERE / "gen.py",
+              HERE / "harness.cpp", gen.INCLUDE / "silvann_gfx950_attention.h"]:
+        h.update(f.read_bytes())
+    return h.hexdigest()[:16]
+
+
+def build() -> Path:
+    from . import gen
+    cxx = compiler()
+    if cxx is None:
+        raise RuntimeError("no clang++ for the emulation")
+    key = _digest()
+    exe = BUILD / f"emu-{key}"
+    if exe.exists():
+        return exe
+    srcs = gen.write(BUILD, SOURCES) + [HERE / "harness.cpp"]
+
+    def cc(src: Path) -> Path:
+        obj = BUILD / (src.stem + f"-{key}.o")
+        subprocess.run([cxx, *FLAGS, f"-I{BUILD}", f"-I{gen.INCLUDE}", "-c", str(src), "-o", str(obj)], check=True)
+        return obj
+
+    with cf.ThreadPoolExecutor(max_workers=len(srcs)) as ex:
+        objs = list(ex.map(cc, srcs))
+    tmp = exe.with_suffix(".tmp")
+    subprocess.run([cxx, *FLAGS, *map(str, objs), "-o", str(tmp)], check=True)
+    os.replace(tmp, exe)
+    return exe
+
+
+def _run(files: dict, params: str, env: dict | None, timeout: int) -> tuple[np.ndarray, int, str]:
+    exe = build()
+    with tempfile.TemporaryDirectory(prefix="silvann_emu_") as d:
+        for name, arr in files.items():
+            if arr is not None:
+                np.ascontiguousarray(arr).tofile(f"{d}/{name}.bin")
+        Path(d, "params.txt").write_text(params + f" {timeout}\n")
+        r = subprocess.run([str(exe), d], capture_output=True, text=True, env={**os.environ, **(env or {})},
+                           timeout=timeout + 60)
+        if r.returncode != 0:
+            raise RuntimeError(f"emulation exited {r.returncode}:\n{r.stderr[-4000:]}")
+        out = np.fromfile(f"{d}/o.bin", dtype=np.float16)
+        over = int(np.fromfile(f"{d}/over.bin", dtype=np.uint32)[0])
+        return out, over, r.stderr
+
+
+def run_causal(w, env: dict | None = None, timeout: int = 900):
+    pages = None if w.pages is None else w.pages.astype(np.uint32)
+    params = f"causal {w.q_heads} {w.kv_heads} {w.head_dim} {w.first} {w.rows} {w.page_size} 0 0"
+    return _run({"q": w.q, "k": w.k, "v": w.v, "pages": pages}, params, env, timeout)
+
+
+def run_decode(w, env: dict | None = None, timeout: int = 900):
+    pages = None if w.pages is None else w.pages.astype(np.uint32)
+    params = (f"decode {w.q_heads} {w.kv_heads} {w.head_dim} {w.most} {w.rows} {w.page_size} {w.pages_row} "
+              f"{w.k_row}")
+    return _run({"q": w.q, "k": w.k, "v": w.v, "pages": pages, "lens": w.lens.astype(np.uint32)}, params, env,
+                timeout)

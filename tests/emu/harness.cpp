@@ -1,0 +1,123 @@
+// harness.cpp — TEST INFRASTRUCTURE: runs one call of the library's causal-prefill or paged-decode entry
+// point in the CPU emulation, on inputs and parameters a test wrote to a directory, and writes the answer
+// back there. Every buffer sits against an inaccessible page, so an out-of-bounds read or write stops the
+// run with the buffer, the offset and the lane that made it; a run that outlives its time limit (a lost
+// barrier) stops too.
+#include <execinfo.h>
+#include <signal.h>
+#include <sys/mman.h>
+#include <unistd.h>
+
+#include <string>
+
+#include "emu_rt.hpp"
+#include "silvann_gfx950_attention.h"
+
+namespace silvann { extern int emu_refused; }
+
+namespace {
+struct Guarded { char* map; size_t len; char* p; size_t n; const char* name; };
+std::vector<Guarded> bufs;
+
+char* guarded(size_t n, const char* name) {
+    const size_t pg = 4096, body = (n + pg - 1) / pg * pg, len = body + 2 * pg;
+    char* m = (char*)mmap(nullptr, len, PROT_READ | PROT_WRITE, MAP_PRIVATE | MAP_ANONYMOUS, -1, 0);
+    if (m == MAP_FAILED) abort();
+    mprotect(m, pg, PROT_NONE);
+    mprotect(m + pg + body, pg, PROT_NONE);
+    char* p = m + pg + body - n;   // the buffer ends at the upper guard page
+    bufs.push_back({m, len, p, n, name});
+    return p;
+}
+
+void on_fault(int sig, siginfo_t* si, void*) {
+    char msg[512];
+    const char* who = "no buffer";
+    long rel = 0;
+    for (auto& b : bufs)
+        if ((char*)si->si_addr >= b.map && (char*)si->si_addr < b.map + b.len) {
+            who = b.name;
+            rel = (char*)si->si_addr - b.p;
+        }
+    const int k = snprintf(msg, sizeof msg, "EMU FAULT signal %d at %p (%s, offset %ld) lane %u block (%u,%u,%u)\n",
+                           sig, si->si_addr, who, rel, threadIdx.x, blockIdx.x, blockIdx.y, blockIdx.z);
+    (void)!write(2, msg, k);
+    void* bt[64];
+    backtrace_symbols_fd(bt, backtrace(bt, 64), 2);
+    _exit(3);
+}
+
+void on_alarm(int) {
+    const char m[] = "EMU TIMEOUT (a barrier some lanes never reach?)\n";
+    (void)!write(2, m, sizeof m - 1);
+    _exit(4);
+}
+
+char* load(const std::string& f, const char* name, size_t* n = nullptr) {
+    FILE* fp = fopen(f.c_str(), "rb");
+    if (!fp) return nullptr;
+    fseek(fp, 0, SEEK_END);
+    const size_t len = ftell(fp);
+    fseek(fp, 0, SEEK_SET);
+    char* p = guarded(len, name);
+    if (fread(p, 1, len, fp) != len) abort();
+    fclose(fp);
+    if (n) *n = len;
+    return p;
+}
+
+void save(const std::string& f, const void* p, size_t n) {
+    FILE* fp = fopen(f.c_str(), "wb");
+    fwrite(p, 1, n, fp);
+    fclose(fp);
+}
+}  // namespace
+
+int main(int argc, char** argv) {
+    if (argc != 2) return 2;
+    struct sigaction sa {};
+    sa.sa_sigaction = on_fault;
+    sa.sa_flags = SA_SIGINFO;
+    sigaction(SIGSEGV, &sa, nullptr);
+    sigaction(SIGBUS, &sa, nullptr);
+    signal(SIGALRM, on_alarm);
+    const std::string d = argv[1];
+    char mode[16];
+    unsigned long qh, kvh, hd, a0, a1, ps, pages_row, k_row, timeout;
+    FILE* fp = fopen((d + "/params.txt").c_str(), "r");
+    if (!fp || fscanf(fp, "%15s %lu %lu %lu %lu %lu %lu %lu %lu %lu", mode, &qh, &kvh, &hd, &a0, &a1, &ps, &pages_row,
+                      &k_row, &timeout) != 10)
+        return 2;
+    fclose(fp);
+    alarm((unsigned)timeout);
+    char* q = load(d + "/q.bin", "q");
+    char* k = load(d + "/k.bin", "k");
+    char* v = load(d + "/v.bin", "v");
+    char* pages = load(d + "/pages.bin", "pages");
+    unsigned int* over = (unsigned int*)guarded(4, "over");
+    *over = 0;
+    size_t on = 0;
+    char* o = nullptr;
+    if (std::string(mode) == "causal") {   // a0 = first, a1 = rows
+        on = a1 * qh * hd * 2;
+        o = guarded(on, "o");
+        memset(o, 0, on);
+        silvann_gfx950_attention_causal_paged((uint16_t*)o, (const uint16_t*)q, (const uint16_t*)k, (const uint16_t*)v,
+                                              (const uint32_t*)pages, ps, qh, kvh, hd, a0, a1, over);
+    } else {                               // a0 = most, a1 = rows
+        char* lens = load(d + "/lens.bin", "lens");
+        on = a1 * qh * hd * 2;
+        o = guarded(on, "o");
+        memset(o, 0, on);
+        const uint64_t sb = silvann_gfx950_attention_decode_paged_scratch(qh, kvh, hd, a0, a1);
+        float* scratch = (float*)guarded(sb ? sb : 4, "scratch");
+        memset(scratch, 0xFF, sb ? sb : 4);   // whatever a caller's scratch held before
+        silvann_gfx950_attention_decode_paged((uint16_t*)o, (const uint16_t*)q, (const uint16_t*)k, (const uint16_t*)v,
+                                              (const uint32_t*)pages, pages_row, ps, k_row, (const uint32_t*)lens, qh, kvh,
+                                              hd, a0, a1, scratch, over);
+    }
+    save(d + "/o.bin", o, on);
+    save(d + "/over.bin", over, 4);
+    fprintf(stderr, "emu done: refused %d, wave exchanges %ld\n", silvann::emu_refused, (long)emu::ops);
+    return silvann::emu_refused ? 5 : 0;
+}

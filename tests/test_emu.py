@@ -1,0 +1,61 @@
+"""The library's kernel sources run in the CPU emulation (tests/emu) against the oracle — no GPU needed.
+
+The emulation (tests/emu/emu_rt.hpp) runs every lane of a workgroup as a host thread with the gfx950
+operand layouts of the MFMA and the transposing LDS read; direct-to-LDS loads land only when the issuing
+lane's s_waitcnt lets them (their destination reads NaN before that), and every buffer sits against a guard
+page. So these tests check the kernels' arithmetic, their waits and barriers, and that every access stays
+inside its buffer, through the same C entry points the GPU tests call. The bar is the GPU tests' bar:
+max-abs <= 2e-3 and cosine >= 0.9999 on the fp16 outputs (tests/conftest.py::parity). They do not measure
+anything a GPU would: timing, and hardware behaviour the emulation does not model.
+
+Shapes are small (the emulation runs a few workgroups a second).
+"""
+import numpy as np
+import pytest
+
+from silvann_amd import workloads as W
+from tests.conftest import parity
+from tests.emu import emu
+
+pytestmark = pytest.mark.skipif(emu.compiler() is None, reason="no clang++ for the CPU emulation")
+
+PIPE = {"SILVANN_GFX950_PREFILL": "pipe"}
+
+
+def _causal(oracle, hd, qh, kvh, first, rows, ps, env=None):
+    w = W.causal("emu", qh, kvh, hd, first, rows, page_size=ps, seed=hd + rows)
+    got, over, _ = emu.run_causal(w, env)
+    want, _ = oracle.causal_rows(w.q, w.k, w.v, w.pages, w.page_size, qh, kvh, hd, first, list(range(rows)))
+    parity(got, want)
+    assert over == 0
+
+
+@pytest.mark.parametrize("hd,qh,kvh,first,rows,ps", [
+    (128, 6, 2, 10, 70, 0),      # group 3: one head a wave, waves on different rows
+    (256, 16, 2, 77, 95, 64),    # paged, page table in LDS, the steady loop at head_dim 256
+])
+def test_causal_default_kernel(oracle, hd, qh, kvh, first, rows, ps):
+    _causal(oracle, hd, qh, kvh, first, rows, ps)
+
+
+@pytest.mark.parametrize("hd,qh,kvh,first,rows,ps", [
+    (256, 16, 2, 0, 130, 0),     # paired row tiles; the first tile load of K 4 must wait for S(0)
+    (256, 6, 2, 37, 90, 0),      # one head a wave: waves with different steady lengths
+    (256, 4, 2, 50, 100, 32),    # two heads a wave, 32-position pages
+])
+def test_causal_pipe_kernel(oracle, hd, qh, kvh, first, rows, ps):
+    _causal(oracle, hd, qh, kvh, first, rows, ps, env=PIPE)
+
+
+@pytest.mark.parametrize("qh,kvh,hd,lens,ps", [
+    (16, 2, 256, [700, 2048], 256),        # paged rows of different lengths
+    (8, 2, 128, [1, 17, 300], 0),          # contiguous, a one-position row
+    (4, 4, 64, [33, 250], 16),             # pages shorter than a tile: one lookup a 16-key group
+])
+def test_decode(oracle, qh, kvh, hd, lens, ps):
+    w = W.decode("emu", qh, kvh, hd, lens, page_size=ps, seed=hd + len(lens))
+    got, over, _ = emu.run_decode(w)
+    want, _ = oracle.decode_paged(w.q, w.k, w.v, w.pages, w.pages_row, w.page_size, w.k_row, w.lens, qh, kvh, hd,
+                                  w.rows)
+    parity(got, want)
+    assert over == 0
