@@ -62,6 +62,22 @@ void silvann_gfx950_attention_causal_scores(float* p, const uint16_t* q, const u
 void silvann_gfx950_attention_causal_mix(uint16_t* o, const float* p, const uint16_t* v, uint64_t q_heads,
                                          uint64_t kv_heads, uint64_t head_dim, uint64_t first, uint64_t rows,
                                          unsigned int* over);
+/* gpu.cuh:163 attention_weights_tq — kernels.cuh:2963-3000: attention_weights over TurboQuant keys. Key row t of kv
+ * head g is row t·kv_heads + g of `codes` (ceil(head_dim / (16/d)) 16-bit containers, little-endian, value c at
+ * bit d·(c % (16/d)) of container c / (16/d)) and `scales` (fp16); value c means level_d[code] · scale, level_d the
+ * reference's table for width d (kernels.cuh:2264-2354, 2650-2653). d is 1, 2, 3, 4, 5 or 8; `codes` 2-byte
+ * aligned; other operands are refused. `q` is already rotated (the caller's). */
+#define SILVANN_GFX950_ROW_ATTENTION_WEIGHTS_TQ 69u
+void silvann_gfx950_attention_weights_tq(float* p, float* res, const uint16_t* q, const uint8_t* codes,
+                                         const uint16_t* scales, uint64_t q_heads, uint64_t kv_heads,
+                                         uint64_t head_dim, uint64_t length, uint64_t d);
+/* gpu.cuh:164 attention_residual_mix_tq — kernels.cuh:3005-3026: res[h].acc[e] = Σ_t p[h][t] · value_t[e] over
+ * TurboQuant values. As the reference allows (kernels.cuh:3001-3003), the door keeps partial sums in `p` once it has
+ * read it: `p` holds no weights afterwards. */
+#define SILVANN_GFX950_ROW_ATTENTION_RESIDUAL_MIX_TQ 70u
+void silvann_gfx950_attention_residual_mix_tq(float* res, const float* p, const uint8_t* codes,
+                                              const uint16_t* scales, uint64_t q_heads, uint64_t kv_heads,
+                                              uint64_t head_dim, uint64_t length, uint64_t d);
 /* gpu.cuh:189 attention_scores_grouped — kernels.cuh:928-948: raw scaled scores, no softmax */
 #define SILVANN_GFX950_ROW_ATTENTION_SCORES_GROUPED 95u
 void silvann_gfx950_attention_scores_grouped(float* p, const uint16_t* q, const uint16_t* k, uint64_t q_heads,
@@ -87,6 +103,17 @@ void silvann_gfx950_attention_weights_rows(float* p, float* res, const uint16_t*
 void silvann_gfx950_attention_residual_mix_rows(float* res, const float* p, const uint16_t* v, uint64_t q_heads,
                                                 uint64_t kv_heads, uint64_t head_dim, uint64_t first,
                                                 uint64_t rows);
+/* gpu.cuh:197 attention_weights_tq_rows — doors.cuh:203,433-441: weights_tq for `rows` queries over the same keys,
+ * row r's q at q + r·q_heads·head_dim, weights at p + r·q_heads·length, residuals at res + r·q_heads·(head_dim + 2) */
+#define SILVANN_GFX950_ROW_ATTENTION_WEIGHTS_TQ_ROWS 103u
+void silvann_gfx950_attention_weights_tq_rows(float* p, float* res, const uint16_t* q, const uint8_t* codes,
+                                              const uint16_t* scales, uint64_t q_heads, uint64_t kv_heads,
+                                              uint64_t head_dim, uint64_t length, uint64_t d, uint64_t rows);
+/* gpu.cuh:198 attention_residual_mix_tq_rows — doors.cuh:204,442-450 (p holds no weights afterwards, as above) */
+#define SILVANN_GFX950_ROW_ATTENTION_RESIDUAL_MIX_TQ_ROWS 104u
+void silvann_gfx950_attention_residual_mix_tq_rows(float* res, const float* p, const uint8_t* codes,
+                                                   const uint16_t* scales, uint64_t q_heads, uint64_t kv_heads,
+                                                   uint64_t head_dim, uint64_t length, uint64_t d, uint64_t rows);
 /* gpu.cuh:222 attention_scores_grouped_rows — kernels.cuh:953-972: row u's lens[u] keys at k + u·k_row */
 #define SILVANN_GFX950_ROW_ATTENTION_SCORES_GROUPED_ROWS 128u
 void silvann_gfx950_attention_scores_grouped_rows(float* p, uint64_t p_row, const uint16_t* q, uint64_t q_row,

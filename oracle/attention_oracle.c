@@ -361,6 +361,96 @@ void oracle_attention_residual_mix_rows(float* res, const float* p, const uint16
                                       first + r + 1);
 }
 
+/* ── TurboQuant rows: keys and values as d-bit codes with one fp16 scale a row ─────────────────────── */
+
+/* kernels.cuh:2810-2817 — a container is 16 bits holding 16 / d codes; a row is whole containers. */
+static uint64_t tq_per(uint64_t d) { return 16u / d; }
+uint64_t oracle_tq_row_bytes(uint64_t d, uint64_t cols) {
+    const uint64_t per = tq_per(d);
+    return ((cols + per - 1u) / per) * 2u;
+}
+
+/* kernels.cuh:2957-2961 (+ level, 2650-2653) — element c of a row: its code's level times the row's scale.
+ * `levels` is width d's table as fp16 bits (the test passes the reference's, read through its own door). */
+static float tq_element(const uint8_t* row, float scale, uint64_t d, uint64_t c, const uint16_t* levels) {
+    const uint64_t per = tq_per(d);
+    const uint32_t unit = (uint32_t)row[(c / per) * 2u] | ((uint32_t)row[(c / per) * 2u + 1u] << 8);
+    return scale * h2f(levels[(unit >> (uint32_t)(d * (c % per))) & ((1u << (uint32_t)d) - 1u)]);
+}
+
+/* kernels.cuh:2963-3000 — the first pass over TurboQuant keys (row t·kv_heads + g): scaled dots, then
+ * e^(s - m) unnormalised into p and {m, l} into res. The body's word-at-a-time path takes the same products
+ * in the same order, so the serial form is both. */
+void oracle_attention_weights_tq(float* p, float* res, const uint16_t* q, const uint8_t* codes,
+                                 const uint16_t* scales, uint64_t q_heads, uint64_t kv_heads, uint64_t head_dim,
+                                 uint64_t length, uint64_t d, const uint16_t* levels) {
+    const uint64_t group = q_heads / kv_heads, row_bytes = oracle_tq_row_bytes(d, head_dim), w = head_dim + 2;
+    const float inv = 1.0f / sqrtf((float)(uint32_t)head_dim);
+    for (uint64_t h = 0; h < q_heads; ++h) {
+        const uint16_t* qh = q + h * head_dim;
+        const uint64_t g = h / group;
+        float* ph = p + h * length;
+        float top = -INFINITY;
+        for (uint64_t t = 0; t < length; ++t) {
+            const uint64_t r = t * kv_heads + g;
+            const uint8_t* kr = codes + r * row_bytes;
+            const float scale = h2f(scales[r]);
+            float dot = 0.0f;
+            for (uint64_t e = 0; e < head_dim; ++e) dot += h2f(qh[e]) * tq_element(kr, scale, d, e, levels);
+            ph[t] = dot * inv;
+            if (ph[t] > top) top = ph[t];
+        }
+        float part = 0.0f;
+        for (uint64_t t = 0; t < length; ++t) {
+            ph[t] = expf(ph[t] - top);
+            part += ph[t];
+        }
+        res[h * w] = top;
+        res[h * w + 1] = part;
+    }
+}
+
+/* kernels.cuh:3005-3026 — its second pass: acc[e] = sum_t p[t] · value_t[e], the values TurboQuant rows. */
+void oracle_attention_residual_mix_tq(float* res, const float* p, const uint8_t* codes, const uint16_t* scales,
+                                      uint64_t q_heads, uint64_t kv_heads, uint64_t head_dim, uint64_t length,
+                                      uint64_t d, const uint16_t* levels) {
+    const uint64_t group = q_heads / kv_heads, row_bytes = oracle_tq_row_bytes(d, head_dim), w = head_dim + 2;
+    for (uint64_t h = 0; h < q_heads; ++h) {
+        const float* ph = p + h * length;
+        const uint64_t g = h / group;
+        float* acc = res + h * w + 2;
+        for (uint64_t e = 0; e < head_dim; ++e) {
+            float sum = 0.0f;
+            for (uint64_t t = 0; t < length; ++t) {
+                const uint64_t r = t * kv_heads + g;
+                sum += ph[t] * tq_element(codes + r * row_bytes, h2f(scales[r]), d, e, levels);
+            }
+            acc[e] = sum;
+        }
+    }
+}
+
+/* doors.cuh:433-441 — weights_tq a row at a time: row r's queries at q + r·q_heads·head_dim, all over the same
+ * `length` keys, its weights at p + r·q_heads·length, its residuals at res + r·q_heads·(head_dim + 2). */
+void oracle_attention_weights_tq_rows(float* p, float* res, const uint16_t* q, const uint8_t* codes,
+                                      const uint16_t* scales, uint64_t q_heads, uint64_t kv_heads,
+                                      uint64_t head_dim, uint64_t length, uint64_t d, uint64_t rows,
+                                      const uint16_t* levels) {
+    for (uint64_t r = 0; r < rows; ++r)
+        oracle_attention_weights_tq(p + r * q_heads * length, res + r * q_heads * (head_dim + 2),
+                                    q + r * q_heads * head_dim, codes, scales, q_heads, kv_heads, head_dim, length, d,
+                                    levels);
+}
+
+/* doors.cuh:442-450 */
+void oracle_attention_residual_mix_tq_rows(float* res, const float* p, const uint8_t* codes, const uint16_t* scales,
+                                           uint64_t q_heads, uint64_t kv_heads, uint64_t head_dim, uint64_t length,
+                                           uint64_t d, uint64_t rows, const uint16_t* levels) {
+    for (uint64_t r = 0; r < rows; ++r)
+        oracle_attention_residual_mix_tq(res + r * q_heads * (head_dim + 2), p + r * q_heads * length, codes, scales,
+                                         q_heads, kv_heads, head_dim, length, d, levels);
+}
+
 /* ── paged forms (the reference has none: its answer over the gathered-contiguous cache) ───────────── */
 
 /* Positions [0, length) of a paged plane gathered into `out` as [position][kv_heads][head_dim]. */

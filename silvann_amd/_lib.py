@@ -25,12 +25,16 @@ SIGNATURES = {
     "silvann_gfx950_attention_finish": [_p, _p, _u64, _u64, _p],
     "silvann_gfx950_attention_causal_scores": [_p, _p, _p, _u64, _u64, _u64, _u64, _u64],
     "silvann_gfx950_attention_causal_mix": [_p, _p, _p, _u64, _u64, _u64, _u64, _u64, _p],
+    "silvann_gfx950_attention_weights_tq": [_p, _p, _p, _p, _p, _u64, _u64, _u64, _u64, _u64],
+    "silvann_gfx950_attention_residual_mix_tq": [_p, _p, _p, _p, _u64, _u64, _u64, _u64, _u64],
     "silvann_gfx950_attention_scores_grouped": [_p, _p, _p, _u64, _u64, _u64, _u64],
     "silvann_gfx950_attention_softmax_rows": [_p, _u64, _u64],
     "silvann_gfx950_attention_causal_scores_grouped": [_p, _p, _p, _u64, _u64, _u64, _u64, _u64],
     "silvann_gfx950_attention_causal_softmax": [_p, _u64, _u64, _u64],
     "silvann_gfx950_attention_weights_rows": [_p, _p, _p, _p, _u64, _u64, _u64, _u64, _u64],
     "silvann_gfx950_attention_residual_mix_rows": [_p, _p, _p, _u64, _u64, _u64, _u64, _u64],
+    "silvann_gfx950_attention_weights_tq_rows": [_p, _p, _p, _p, _p, _u64, _u64, _u64, _u64, _u64, _u64],
+    "silvann_gfx950_attention_residual_mix_tq_rows": [_p, _p, _p, _p, _u64, _u64, _u64, _u64, _u64, _u64],
     "silvann_gfx950_attention_scores_grouped_rows": [_p, _u64, _p, _u64, _p, _u64, _p, _u64, _u64, _u64, _u64, _u64],
     "silvann_gfx950_attention_softmax_lens": [_p, _u64, _p, _u64, _u64],
     "silvann_gfx950_attention_mix_rows": [_p, _u64, _p, _u64, _p, _u64, _p, _u64, _u64, _u64, _u64, _p],

@@ -19,6 +19,7 @@
 #include <stdio.h>
 
 #include "common.hpp"
+#include "tq_levels.hpp"
 #include "../../include/silvann_gfx950_attention.h"
 
 namespace silvann {
@@ -32,6 +33,8 @@ enum Mode : int {
                        //   p u·p_row + h·len, o u·o_row
     kByRow = 3,        // the one-row door a row at a time (weights_rows, residual_mix_rows, doors.cuh:417-432):
                        //   len first+r+1, q row r·qh·hd, p r·qh·span + h·len, res (r·qh+h)·(hd+2)
+    kTqRows = 4,       // the TurboQuant rows (weights_tq_rows, residual_mix_tq_rows, doors.cuh:433-450): every row
+                       //   over the same `length` keys; q row r·qh·hd, p r·qh·len + h·len, res (r·qh+h)·(hd+2)
 };
 
 struct Geom {
@@ -58,6 +61,9 @@ __device__ __forceinline__ RowAt row_at(const Geom& G, uint64_t u) {
         r.o = u * G.o_row;
     } else if constexpr (MODE == kByRow) {
         r.len = G.first + u + 1; r.q = u * qh * hd; r.k = 0; r.p = u * qh * G.span; r.hstride = r.len;
+        r.o = u * qh * (hd + 2);
+    } else if constexpr (MODE == kTqRows) {
+        r.len = G.length; r.q = u * qh * hd; r.k = 0; r.p = u * qh * G.length; r.hstride = G.length;
         r.o = u * qh * (hd + 2);
     } else {
         static_assert(MODE == kSingle, "row geometry");
@@ -302,6 +308,201 @@ void launch_mix(uint16_t* o, float* acc_out, const float* p, const uint16_t* v, 
     }
 }
 
+
+// ── TurboQuant rows: keys and values as d-bit codes, one fp16 scale a row (kernels.cuh:2957-3026) ─────
+//
+// A row of head_dim values is ceil(head_dim / (16 / D)) 16-bit containers, value c in container c / (16 / D)
+// at bit D·(c % (16 / D)); it means kTqLevels<D>[code] (fp16) times the row's scale. Key row t of kv head g
+// is row t·kv_heads + g of `codes` / `scales` (kernels.cuh:2972-2974).
+//   tq_scores      a workgroup per (row, kv head, 16-head block, 256 keys); a thread per key decodes its
+//                  row once for all the block's query heads (held in LDS), as scores_raw does for fp16 keys;
+//                  then softmax_rows writes e^(s - m) and {m, l} (kernels.cuh:2963-3000)
+//   tq_mix_part    a workgroup per (row, kv head, 16-head block, split of the keys); a wave per 64 dims, a
+//                  lane per dim, every head of the block from one decode of each value; the split's sums go
+//                  into the workgroup's own stretch of `p` — weights it has finished reading, which the
+//                  reference hands the pass to keep its sums in (kernels.cuh:3001-3003) — or straight into
+//                  the residual when there is one split
+//   tq_mix_reduce  the splits' sums, in split order, into the residual's acc
+
+// Level c of width D as fp16 bits (the tables are device read-only data; each workgroup copies its width's
+// into LDS as floats).
+template <int D> __device__ __forceinline__ uint16_t tq_level_bits(uint32_t c) {
+    if constexpr (D == 1) return kTqLevels1[c];
+    else if constexpr (D == 2) return kTqLevels2[c];
+    else if constexpr (D == 3) return kTqLevels3[c];
+    else if constexpr (D == 4) return kTqLevels4[c];
+    else if constexpr (D == 5) return kTqLevels5[c];
+    else return kTqLevels8[c];
+}
+
+constexpr uint32_t kTqSplit = 1024;   // keys a split of tq_mix_part at least (and at least head_dim: the sums' room)
+
+template <int MODE, int D>
+__global__ __launch_bounds__(256) void tq_scores(float* p, const uint16_t* q, const uint16_t* codes16,
+                                                 const uint16_t* scales, Geom G, uint32_t hblocks, uint32_t nheads,
+                                                 uint32_t row_units, float inv) {
+    constexpr uint32_t PER = 16 / D, MASK = (1u << D) - 1u;
+    extern __shared__ float qs[];   // [nheads][head_dim], then the 2^D levels
+    float* lev = qs + nheads * G.head_dim;
+    const uint64_t u = blockIdx.z;
+    const uint32_t g = blockIdx.y / hblocks, hb = blockIdx.y % hblocks;
+    const uint32_t group = G.q_heads / G.kv_heads, hd = G.head_dim;
+    const uint32_t h0 = g * group + hb * nheads;
+    const int nh = (int)min(nheads, group - hb * nheads);
+    const RowAt R = row_at<MODE>(G, u);
+    const uint64_t t = (uint64_t)blockIdx.x * 256 + threadIdx.x;
+    if ((uint64_t)blockIdx.x * 256 >= R.len) return;
+    for (uint32_t i = threadIdx.x; i < (uint32_t)nh * hd; i += 256)
+        qs[i] = half_bits_to_float(q[R.q + (uint64_t)(h0 + i / hd) * hd + i % hd]);
+    for (uint32_t c = threadIdx.x; c < (1u << D); c += 256) lev[c] = half_bits_to_float(tq_level_bits<D>(c));
+    __syncthreads();
+    if (t >= R.len) return;
+    const uint64_t krow = t * G.kv_heads + g;
+    const uint16_t* kr = codes16 + krow * row_units;
+    const float scale = half_bits_to_float(scales[krow]);
+    float dot[kHB];
+#pragma unroll
+    for (int j = 0; j < kHB; ++j) dot[j] = 0.0f;
+    for (uint32_t w = 0; w < row_units; ++w) {
+        const uint32_t unit = kr[w];
+#pragma unroll
+        for (uint32_t s = 0; s < PER; ++s) {
+            const uint32_t e = w * PER + s;
+            if (e >= hd) break;
+            const float kv = scale * lev[(unit >> (D * s)) & MASK];
+#pragma unroll
+            for (int j = 0; j < kHB; ++j)
+                if (j < nh) dot[j] += qs[j * hd + e] * kv;
+        }
+    }
+#pragma unroll
+    for (int j = 0; j < kHB; ++j)
+        if (j < nh) p[R.p + (uint64_t)(h0 + j) * R.hstride + t] = dot[j] * inv;
+}
+
+// `direct`: one split, its sums straight into the residual; else into p at the split's start (then the
+// launch has head_dim <= 256: one pass of lanes holds every dim, and every lane has read its weights before
+// any lane writes over them).
+template <int MODE, int D>
+__global__ __launch_bounds__(256) void tq_mix_part(float* res, float* p, const uint16_t* codes16,
+                                                   const uint16_t* scales, Geom G, uint32_t hblocks,
+                                                   uint32_t row_units, uint32_t nsplit, uint64_t split, bool direct) {
+    constexpr uint32_t PER = 16 / D, MASK = (1u << D) - 1u;
+    __shared__ float lev[1 << D];
+    const uint64_t u = blockIdx.z;
+    const uint32_t s = blockIdx.x;
+    const uint32_t g = blockIdx.y / hblocks, hb = blockIdx.y % hblocks;
+    const uint32_t group = G.q_heads / G.kv_heads, hd = G.head_dim;
+    const uint32_t h0 = g * group + hb * kHB;
+    const int nh = (int)min((uint32_t)kHB, group - hb * kHB);
+    const RowAt R = row_at<MODE>(G, u);
+    const uint64_t t0 = (uint64_t)s * split, t1 = s + 1 == nsplit ? R.len : t0 + split;
+    for (uint32_t c = threadIdx.x; c < (1u << D); c += 256) lev[c] = half_bits_to_float(tq_level_bits<D>(c));
+    __syncthreads();
+    const float* pb = p + R.p + (uint64_t)h0 * R.hstride;
+    for (uint32_t base = 0; base < hd; base += 256) {   // a lane a dim, 256 dims a pass
+        const uint32_t d = base + threadIdx.x;
+        float acc[kHB];
+#pragma unroll
+        for (int j = 0; j < kHB; ++j) acc[j] = 0.0f;
+        if (d < hd) {
+            const uint32_t wunit = d / PER, shift = D * (d % PER);
+            for (uint64_t t = t0; t < t1; ++t) {
+                const uint64_t vrow = t * G.kv_heads + g;
+                const float vv =
+                    half_bits_to_float(scales[vrow]) * lev[(codes16[vrow * row_units + wunit] >> shift) & MASK];
+#pragma unroll
+                for (int j = 0; j < kHB; ++j)
+                    if (j < nh) acc[j] += pb[(uint64_t)j * R.hstride + t] * vv;
+            }
+        }
+        __syncthreads();
+        if (d < hd)
+            for (int j = 0; j < nh; ++j) {
+                if (direct) res[R.o + (uint64_t)(h0 + j) * (hd + 2) + 2 + d] = acc[j];
+                else p[R.p + (uint64_t)(h0 + j) * R.hstride + t0 + d] = acc[j];
+            }
+    }
+}
+
+template <int MODE>
+__global__ __launch_bounds__(256) void tq_mix_reduce(float* res, const float* p, Geom G, uint32_t nsplit,
+                                                     uint64_t split) {
+    const uint64_t u = blockIdx.z;
+    const uint32_t h = blockIdx.y, d = blockIdx.x * 256 + threadIdx.x;
+    const uint32_t hd = G.head_dim;
+    if (d >= hd) return;
+    const RowAt R = row_at<MODE>(G, u);
+    const float* ph = p + R.p + (uint64_t)h * R.hstride + d;
+    float sum = 0.0f;
+    for (uint32_t s = 0; s < nsplit; ++s) sum += ph[(uint64_t)s * split];
+    res[R.o + (uint64_t)h * (hd + 2) + 2 + d] = sum;
+}
+
+
+bool tq_ok(const char* door, const uint8_t* codes, uint64_t head_dim, uint64_t d) {
+    if (!(d == 1 || d == 2 || d == 3 || d == 4 || d == 5 || d == 8) || (((uintptr_t)codes) & 1u) != 0 || head_dim == 0) {
+        refuse(door);
+        return false;
+    }
+    return true;
+}
+
+uint32_t tq_row_units(uint64_t d, uint64_t head_dim) { return (uint32_t)((head_dim + 16 / d - 1) / (16 / d)); }
+
+template <int MODE>
+void launch_tq_scores(float* p, const uint16_t* q, const uint8_t* codes, const uint16_t* scales, const Geom& G,
+                      uint64_t rows, uint64_t d) {
+    if (rows == 0 || G.length == 0) return;
+    const uint32_t group = G.q_heads / G.kv_heads;
+    uint32_t nheads = kHB;   // query heads a block holds, with the levels, in 64 KB of LDS
+    while (nheads > 1 && (uint64_t)nheads * G.head_dim * 4 + (4u << d) > 65536) nheads >>= 1;
+    const uint32_t hblocks = (group + nheads - 1) / nheads;
+    const dim3 grid((uint32_t)((G.length + 255) / 256), G.kv_heads * hblocks, (uint32_t)rows);
+    const size_t lds = (size_t)nheads * G.head_dim * 4 + (4u << d);
+    const float inv = 1.0f / sqrtf((float)(uint32_t)G.head_dim);
+    const uint32_t units = tq_row_units(d, G.head_dim);
+    const uint16_t* c16 = (const uint16_t*)codes;
+    hipStream_t st = stream();
+    switch (d) {
+        case 1: tq_scores<MODE, 1><<<grid, 256, lds, st>>>(p, q, c16, scales, G, hblocks, nheads, units, inv); break;
+        case 2: tq_scores<MODE, 2><<<grid, 256, lds, st>>>(p, q, c16, scales, G, hblocks, nheads, units, inv); break;
+        case 3: tq_scores<MODE, 3><<<grid, 256, lds, st>>>(p, q, c16, scales, G, hblocks, nheads, units, inv); break;
+        case 4: tq_scores<MODE, 4><<<grid, 256, lds, st>>>(p, q, c16, scales, G, hblocks, nheads, units, inv); break;
+        case 5: tq_scores<MODE, 5><<<grid, 256, lds, st>>>(p, q, c16, scales, G, hblocks, nheads, units, inv); break;
+        default: tq_scores<MODE, 8><<<grid, 256, lds, st>>>(p, q, c16, scales, G, hblocks, nheads, units, inv); break;
+    }
+}
+
+template <int MODE>
+void launch_tq_mix(float* res, float* p, const uint8_t* codes, const uint16_t* scales, const Geom& G, uint64_t rows,
+                   uint64_t d) {
+    if (rows == 0) return;
+    const uint32_t group = G.q_heads / G.kv_heads;
+    const uint32_t hblocks = (group + kHB - 1) / kHB;
+    // splits of `split` keys, the last taking the remainder (so each has at least `split` >= head_dim keys of
+    // room for its sums); at most 65535 of them. Splitting needs head_dim <= 256 (one pass of lanes).
+    uint64_t split = kTqSplit;
+    while (G.length / split > 65535) split *= 2;
+    const uint32_t nsplit = G.head_dim <= 256 && G.length >= 2 * split ? (uint32_t)(G.length / split) : 1u;
+    const bool direct = nsplit == 1;
+    const dim3 grid(nsplit, G.kv_heads * hblocks, (uint32_t)rows);
+    const uint32_t units = tq_row_units(d, G.head_dim);
+    const uint16_t* c16 = (const uint16_t*)codes;
+    hipStream_t st = stream();
+    switch (d) {
+        case 1: tq_mix_part<MODE, 1><<<grid, 256, 0, st>>>(res, p, c16, scales, G, hblocks, units, nsplit, split, direct); break;
+        case 2: tq_mix_part<MODE, 2><<<grid, 256, 0, st>>>(res, p, c16, scales, G, hblocks, units, nsplit, split, direct); break;
+        case 3: tq_mix_part<MODE, 3><<<grid, 256, 0, st>>>(res, p, c16, scales, G, hblocks, units, nsplit, split, direct); break;
+        case 4: tq_mix_part<MODE, 4><<<grid, 256, 0, st>>>(res, p, c16, scales, G, hblocks, units, nsplit, split, direct); break;
+        case 5: tq_mix_part<MODE, 5><<<grid, 256, 0, st>>>(res, p, c16, scales, G, hblocks, units, nsplit, split, direct); break;
+        default: tq_mix_part<MODE, 8><<<grid, 256, 0, st>>>(res, p, c16, scales, G, hblocks, units, nsplit, split, direct); break;
+    }
+    if (!direct) {
+        const dim3 rgrid((G.head_dim + 255) / 256, G.q_heads, (uint32_t)rows);
+        tq_mix_reduce<MODE><<<rgrid, 256, 0, st>>>(res, p, G, nsplit, split);
+    }
+}
 }  // namespace
 }  // namespace silvann
 
@@ -494,4 +695,64 @@ SILVANN_EXPORT void silvann_gfx950_attention_mix_rows(uint16_t* o, uint64_t o_ro
     G.p_row = p_row; G.k_row = v_row; G.o_row = o_row; G.lens = lens;
     launch_mix(o, nullptr, p, v, G, rows, over);
     check_launch("attention_mix_rows");
+}
+
+// gpu.cuh:163 attention_weights_tq — kernels.cuh:2963-3000: e^(s - m) unnormalised into p, {m, l} into res
+SILVANN_EXPORT void silvann_gfx950_attention_weights_tq(float* p, float* res, const uint16_t* q, const uint8_t* codes,
+                                                        const uint16_t* scales, uint64_t q_heads, uint64_t kv_heads,
+                                                        uint64_t head_dim, uint64_t length, uint64_t d) {
+    if (!heads_ok("attention_weights_tq", q_heads, kv_heads, head_dim, 1) ||
+        !tq_ok("attention_weights_tq", codes, head_dim, d))
+        return;
+    Geom G = geom(kSingle, q_heads, kv_heads, head_dim);
+    G.length = length;
+    launch_tq_scores<kSingle>(p, q, codes, scales, G, 1, d);
+    launch_softmax(p, res, G, q_heads);
+    check_launch("attention_weights_tq");
+}
+
+// gpu.cuh:164 attention_residual_mix_tq — kernels.cuh:3005-3026. The weights are the pass's once read: its
+// splits keep their sums in p (kernels.cuh:3001-3003), so p holds no weights after it.
+SILVANN_EXPORT void silvann_gfx950_attention_residual_mix_tq(float* res, const float* p, const uint8_t* codes,
+                                                             const uint16_t* scales, uint64_t q_heads,
+                                                             uint64_t kv_heads, uint64_t head_dim, uint64_t length,
+                                                             uint64_t d) {
+    if (!heads_ok("attention_residual_mix_tq", q_heads, kv_heads, head_dim, 1) ||
+        !tq_ok("attention_residual_mix_tq", codes, head_dim, d))
+        return;
+    Geom G = geom(kSingle, q_heads, kv_heads, head_dim);
+    G.length = length;
+    launch_tq_mix<kSingle>(res, const_cast<float*>(p), codes, scales, G, 1, d);
+    check_launch("attention_residual_mix_tq");
+}
+
+// gpu.cuh:197 attention_weights_tq_rows — doors.cuh:203,433-441: weights_tq a row at a time, in one launch
+SILVANN_EXPORT void silvann_gfx950_attention_weights_tq_rows(float* p, float* res, const uint16_t* q,
+                                                             const uint8_t* codes, const uint16_t* scales,
+                                                             uint64_t q_heads, uint64_t kv_heads, uint64_t head_dim,
+                                                             uint64_t length, uint64_t d, uint64_t rows) {
+    if (!heads_ok("attention_weights_tq_rows", q_heads, kv_heads, head_dim, rows) ||
+        !tq_ok("attention_weights_tq_rows", codes, head_dim, d))
+        return;
+    Geom G = geom(kTqRows, q_heads, kv_heads, head_dim);
+    G.length = length;
+    launch_tq_scores<kTqRows>(p, q, codes, scales, G, rows, d);
+    Geom S = geom(kSingle, q_heads, kv_heads, head_dim);   // weight row i at i·length, its residual at i·(hd + 2)
+    S.length = length;
+    launch_softmax(p, res, S, rows * q_heads);
+    check_launch("attention_weights_tq_rows");
+}
+
+// gpu.cuh:198 attention_residual_mix_tq_rows — doors.cuh:204,442-450
+SILVANN_EXPORT void silvann_gfx950_attention_residual_mix_tq_rows(float* res, const float* p, const uint8_t* codes,
+                                                                  const uint16_t* scales, uint64_t q_heads,
+                                                                  uint64_t kv_heads, uint64_t head_dim,
+                                                                  uint64_t length, uint64_t d, uint64_t rows) {
+    if (!heads_ok("attention_residual_mix_tq_rows", q_heads, kv_heads, head_dim, rows) ||
+        !tq_ok("attention_residual_mix_tq_rows", codes, head_dim, d))
+        return;
+    Geom G = geom(kTqRows, q_heads, kv_heads, head_dim);
+    G.length = length;
+    launch_tq_mix<kTqRows>(res, const_cast<float*>(p), codes, scales, G, rows, d);
+    check_launch("attention_residual_mix_tq_rows");
 }

@@ -131,12 +131,16 @@ SILVANN_EXPORT uint32_t silvann_gfx950_attention_install(void* nn_doors) {
         {SILVANN_GFX950_ROW_ATTENTION_FINISH, (void*)&silvann_gfx950_attention_finish},
         {SILVANN_GFX950_ROW_ATTENTION_CAUSAL_SCORES, (void*)&silvann_gfx950_attention_causal_scores},
         {SILVANN_GFX950_ROW_ATTENTION_CAUSAL_MIX, (void*)&silvann_gfx950_attention_causal_mix},
+        {SILVANN_GFX950_ROW_ATTENTION_WEIGHTS_TQ, (void*)&silvann_gfx950_attention_weights_tq},
+        {SILVANN_GFX950_ROW_ATTENTION_RESIDUAL_MIX_TQ, (void*)&silvann_gfx950_attention_residual_mix_tq},
         {SILVANN_GFX950_ROW_ATTENTION_SCORES_GROUPED, (void*)&silvann_gfx950_attention_scores_grouped},
         {SILVANN_GFX950_ROW_ATTENTION_SOFTMAX_ROWS, (void*)&silvann_gfx950_attention_softmax_rows},
         {SILVANN_GFX950_ROW_ATTENTION_CAUSAL_SCORES_GROUPED, (void*)&silvann_gfx950_attention_causal_scores_grouped},
         {SILVANN_GFX950_ROW_ATTENTION_CAUSAL_SOFTMAX, (void*)&silvann_gfx950_attention_causal_softmax},
         {SILVANN_GFX950_ROW_ATTENTION_WEIGHTS_ROWS, (void*)&silvann_gfx950_attention_weights_rows},
         {SILVANN_GFX950_ROW_ATTENTION_RESIDUAL_MIX_ROWS, (void*)&silvann_gfx950_attention_residual_mix_rows},
+        {SILVANN_GFX950_ROW_ATTENTION_WEIGHTS_TQ_ROWS, (void*)&silvann_gfx950_attention_weights_tq_rows},
+        {SILVANN_GFX950_ROW_ATTENTION_RESIDUAL_MIX_TQ_ROWS, (void*)&silvann_gfx950_attention_residual_mix_tq_rows},
         {SILVANN_GFX950_ROW_ATTENTION_SCORES_GROUPED_ROWS, (void*)&silvann_gfx950_attention_scores_grouped_rows},
         {SILVANN_GFX950_ROW_ATTENTION_SOFTMAX_LENS, (void*)&silvann_gfx950_attention_softmax_lens},
         {SILVANN_GFX950_ROW_ATTENTION_MIX_ROWS, (void*)&silvann_gfx950_attention_mix_rows},

@@ -37,12 +37,16 @@ attention_merge = _door("attention_merge")
 attention_finish = _door("attention_finish")
 attention_causal_scores = _door("attention_causal_scores")
 attention_causal_mix = _door("attention_causal_mix")
+attention_weights_tq = _door("attention_weights_tq")
+attention_residual_mix_tq = _door("attention_residual_mix_tq")
 attention_scores_grouped = _door("attention_scores_grouped")
 attention_softmax_rows = _door("attention_softmax_rows")
 attention_causal_scores_grouped = _door("attention_causal_scores_grouped")
 attention_causal_softmax = _door("attention_causal_softmax")
 attention_weights_rows = _door("attention_weights_rows")
 attention_residual_mix_rows = _door("attention_residual_mix_rows")
+attention_weights_tq_rows = _door("attention_weights_tq_rows")
+attention_residual_mix_tq_rows = _door("attention_residual_mix_tq_rows")
 attention_scores_grouped_rows = _door("attention_scores_grouped_rows")
 attention_softmax_lens = _door("attention_softmax_lens")
 attention_mix_rows = _door("attention_mix_rows")

@@ -97,6 +97,32 @@ def residual(q, k, v, scores, res, q_heads, kv_heads, head_dim, from_, to):
     return res
 
 
+def tq_row_bytes(d: int, cols: int) -> int:
+    """kernels.cuh:2814-2817: a TurboQuant row of `cols` values is whole 16-bit containers of 16 / d codes."""
+    per = 16 // d
+    return (cols + per - 1) // per * 2
+
+
+def residual_tq(q, k_codes, k_scales, v_codes, v_scales, scores, res, q_heads, kv_heads, head_dim, d, count):
+    """`(nn__attention__residual_tq q kc ks vc vs scores res q_heads kv_heads head_dim d count)` —
+    attention__abi.cuh:245-272: a residual over `count` TurboQuant key and value rows (width d, 4 or 8), the
+    query already rotated. The scores hold no weights afterwards (the mix keeps its sums there)."""
+    q_heads, kv_heads, head_dim = _dim(q_heads), _dim(kv_heads), _dim(head_dim)
+    d, count = _dim(d), _dim(count)
+    if d not in (4, 8) or q_heads % kv_heads:
+        raise Fault(FAULT_TYPE)
+    rows = count * kv_heads
+    code_bytes = rows * tq_row_bytes(d, head_dim)
+    # the reference compares the codes' bytes with their buffers' room as it counts it (attention__abi.cuh:262-265)
+    if (not _fits(q_heads * head_dim, room(q)) or code_bytes > room(k_codes) or not _fits(rows, room(k_scales))
+            or code_bytes > room(v_codes) or not _fits(rows, room(v_scales))
+            or not _fits(2 * q_heads * count, room(scores)) or not _residual_fits(res, q_heads, head_dim)):
+        raise Fault(FAULT_BOUNDS)
+    doors.attention_weights_tq(scores, res, q, k_codes, k_scales, q_heads, kv_heads, head_dim, count, d)
+    doors.attention_residual_mix_tq(res, scores, v_codes, v_scales, q_heads, kv_heads, head_dim, count, d)
+    return res
+
+
 def merge(a, b, into, q_heads, head_dim):
     """`(nn__attention__merge a b into q_heads head_dim)` — attention__abi.cuh:212-227."""
     q_heads, head_dim = _dim(q_heads), _dim(head_dim)

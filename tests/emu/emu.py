@@ -19,7 +19,7 @@ import numpy as np
 
 HERE = Path(__file__).resolve().parent
 BUILD = HERE / "_build"
-SOURCES = ["prefill.hip", "decode.hip"]
+SOURCES = ["prefill.hip", "decode.hip", "doors.hip"]
 CXX_CANDIDATES = ["/opt/rocm/llvm/bin/clang++", "/opt/rocm/lib/llvm/bin/clang++", shutil.which("clang++") or ""]
 FLAGS = ["-std=c++20", "-O1", "-g", "-fno-omit-frame-pointer", "-rdynamic", "-w", "-pthread"]
 
@@ -34,7 +34,8 @@ def compiler() -> str | None:
 def _digest() -> str:
     from . import gen  # noqa: F401  (the transform is part of the key)
     h = hashlib.sha256()
-    for f in [*(gen.CSRC / s for s in SOURCES), gen.CSRC / "common.hpp", HERE / "emu_rt.hpp", HERE / "gen.py",
+    for f in [*(gen.CSRC / s for s in SOURCES), gen.CSRC / "common.hpp", gen.CSRC / "tq_levels.hpp",
+              HERE / "emu_rt.hpp", HERE / "gen.py",
               HERE / "harness.cpp", gen.INCLUDE / "silvann_gfx950_attention.h"]:
         h.update(f.read_bytes())
     return h.hexdigest()[:16]
@@ -53,7 +54,8 @@ def build() -> Path:
 
     def cc(src: Path) -> Path:
         obj = BUILD / (src.stem + f"-{key}.o")
-        subprocess.run([cxx, *FLAGS, f"-I{BUILD}", f"-I{gen.INCLUDE}", "-c", str(src), "-o", str(obj)], check=True)
+        subprocess.run([cxx, *FLAGS, f"-I{BUILD}", f"-I{gen.INCLUDE}", f"-I{gen.CSRC}", "-c", str(src), "-o", str(obj)],
+                       check=True)
         return obj
 
     with cf.ThreadPoolExecutor(max_workers=len(srcs)) as ex:
@@ -64,7 +66,7 @@ def build() -> Path:
     return exe
 
 
-def _run(files: dict, params: str, env: dict | None, timeout: int) -> tuple[np.ndarray, int, str]:
+def _run(files: dict, params: str, env: dict | None, timeout: int, outs=(("o", np.float16),)):
     exe = build()
     with tempfile.TemporaryDirectory(prefix="silvann_emu_") as d:
         for name, arr in files.items():
@@ -75,9 +77,9 @@ def _run(files: dict, params: str, env: dict | None, timeout: int) -> tuple[np.n
                            timeout=timeout + 60)
         if r.returncode != 0:
             raise RuntimeError(f"emulation exited {r.returncode}:\n{r.stderr[-4000:]}")
-        out = np.fromfile(f"{d}/o.bin", dtype=np.float16)
+        got = [np.fromfile(f"{d}/{name}.bin", dtype=dt) for name, dt in outs]
         over = int(np.fromfile(f"{d}/over.bin", dtype=np.uint32)[0])
-        return out, over, r.stderr
+        return (*got, over, r.stderr)
 
 
 def run_causal(w, env: dict | None = None, timeout: int = 900):
@@ -92,3 +94,11 @@ def run_decode(w, env: dict | None = None, timeout: int = 900):
               f"{w.k_row}")
     return _run({"q": w.q, "k": w.k, "v": w.v, "pages": pages, "lens": w.lens.astype(np.uint32)}, params, env,
                 timeout)
+
+
+def run_tq(q, codes, scales, qh, kvh, hd, length, d, rows=0, timeout: int = 900):
+    """weights_tq then residual_mix_tq (their _rows forms when rows > 0): the weights and the residual after the
+    first door, and the residual after the second."""
+    params = f"{'tq_rows' if rows else 'tq'} {qh} {kvh} {hd} {length} {max(rows, 1)} {d} 0 0"
+    return _run({"q": q, "k": codes, "v": scales}, params, None, timeout,
+                outs=(("p", np.float32), ("res_w", np.float32), ("res", np.float32)))

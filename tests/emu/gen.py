@@ -1,7 +1,7 @@
 """TEST INFRASTRUCTURE: turn this library's HIP sources into host C++ for the CPU emulation (emu_rt.hpp).
 
 The kernels are used as they are. The transformation is textual and small: the HIP runtime header and the
-LDS address-space qualifier go, `<<<grid, block, 0, stream>>>(args)` launches become emu::launch calls, and
+LDS address-space qualifier go, `<<<grid, block, lds, stream>>>(args)` launches become emu::launch calls, and
 the few inline-assembly helpers (direct-to-LDS loads, a scalar load, an in-place accumulator scale) become
 their host equivalents. Anything else the emulation does not know stops the build.
 """
@@ -54,20 +54,76 @@ inline void refuse(const char* what) { std::fprintf(stderr, "refused: %s\\n", wh
     return s
 
 
+def _split_top(text: str) -> list[str]:
+    """`text` split at its commas outside any brackets."""
+    parts, depth, cur = [], 0, ""
+    for ch in text:
+        if ch in "([{<":
+            depth += 1
+        elif ch in ")]}>":
+            depth -= 1
+        if ch == "," and depth == 0:
+            parts.append(cur.strip())
+            cur = ""
+        else:
+            cur += ch
+    parts.append(cur.strip())
+    return parts
+
+
+def _launches(s: str) -> str:
+    """`kernel<<<grid, block, lds, stream>>>(args);` -> `emu::launch(grid, block, [&]{ kernel(args); });` (the
+    dynamic LDS size is dropped: dynamic LDS is a static of the most a workgroup may ask for)."""
+    out, i = [], 0
+    while True:
+        j = s.find("<<<", i)
+        if j < 0:
+            out.append(s[i:])
+            return "".join(out)
+        # the kernel name (with template arguments) ends at j; find where it starts
+        k, depth = j, 0
+        while k > 0:
+            ch = s[k - 1]
+            if ch == ">":
+                depth += 1
+            elif ch == "<":
+                depth -= 1
+            elif depth == 0 and not (ch.isalnum() or ch in "_:"):
+                break
+            k -= 1
+        e = s.index(">>>", j)
+        cfg = _split_top(s[j + 3:e])
+        if s[e + 3] != "(":
+            raise RuntimeError("launch without arguments")
+        depth, m = 0, e + 3
+        while True:
+            if s[m] == "(":
+                depth += 1
+            elif s[m] == ")":
+                depth -= 1
+                if depth == 0:
+                    break
+            m += 1
+        out.append(s[i:k])
+        out.append(f"emu::launch({cfg[0]}, {cfg[1]}, [&]{{ {s[k:j]}{s[e + 3:m + 1]}; }})")
+        i = m + 1
+
+
 def kernel(name: str) -> str:
     s = (CSRC / name).read_text()
     s = s.replace('#include "common.hpp"', '#include "common_emu.hpp"')
     s = re.sub(r'#include "\.\./\.\./include/([^"]+)"', lambda m: f'#include "{INCLUDE / m.group(1)}"', s)
     s = s.replace(AS3, "")
     s = re.sub(r"__attribute__\(\(amdgpu_waves_per_eu\([^)]*\)\)\)", "", s)
+    # dynamic LDS: the most a workgroup may ask for, as a static (one workgroup runs at a time)
+    s = re.sub(r"extern __shared__ (\w+) (\w+)\[\];", r"static \1 \2[65536 / sizeof(\1)];", s)
     s = _sub(r"(__device__ __forceinline__ uint32_t scalar_load\(const uint32_t\* p\) \{).*?\n\}",
              r"\1 return *emu_readfirstlane(p); }", s, "scalar_load", required=False)
     s = _sub(r"(__device__ __forceinline__ void scale_acc\(float& x, float c\) \{).*?\n\}", r"\1 x *= c; }", s,
              "scale_acc", required=False)
     s = _sub(r"(__device__ __forceinline__ void dma16s_gap\(const void\* base, uint32_t off, lds_ptr lds\) \{).*?\n\}",
              r"\1 dma16s(base, off, lds); }", s, "dma16s_gap", required=False)
-    s = re.sub(r"(\w+<[^<>;]*>)<<<(\w+), (\w+), 0, (\w+)>>>\(([^;]*)\);", r"emu::launch(\2, \3, [&]{ \1(\5); });", s)
-    s = re.sub(r"(\w+)<<<(\w+), (\w+), 0, (\w+)>>>\(([^;]*)\);", r"emu::launch(\2, \3, [&]{ \1(\5); });", s)
+    s = _launches(s)
     left = [ln for ln in s.splitlines() if re.search(r"\basm\b", ln) or "<<<" in ln]
     if left:
         raise RuntimeError(f"{name}: left for the emulation to handle: {left[:3]}")

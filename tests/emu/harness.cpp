@@ -82,6 +82,7 @@ int main(int argc, char** argv) {
     sigaction(SIGBUS, &sa, nullptr);
     signal(SIGALRM, on_alarm);
     const std::string d = argv[1];
+    auto d_dir = [&](unsigned long) { return d; };
     char mode[16];
     unsigned long qh, kvh, hd, a0, a1, ps, pages_row, k_row, timeout;
     FILE* fp = fopen((d + "/params.txt").c_str(), "r");
@@ -104,6 +105,29 @@ int main(int argc, char** argv) {
         memset(o, 0, on);
         silvann_gfx950_attention_causal_paged((uint16_t*)o, (const uint16_t*)q, (const uint16_t*)k, (const uint16_t*)v,
                                               (const uint32_t*)pages, ps, qh, kvh, hd, a0, a1, over);
+    } else if (std::string(mode) == "tq" || std::string(mode) == "tq_rows") {
+        // a0 = length, a1 = rows, ps = d; k holds the codes, v the scales
+        const unsigned long length = a0, rows = a1, d = ps, rf = hd + 2;
+        float* p = (float*)guarded((rows * qh * length + 1) * 4, "p");
+        float* res = (float*)guarded(rows * qh * rf * 4, "res");
+        memset(res, 0xFF, rows * qh * rf * 4);   // whatever the caller's residual held
+        if (std::string(mode) == "tq")
+            silvann_gfx950_attention_weights_tq(p, res, (const uint16_t*)q, (const uint8_t*)k, (const uint16_t*)v, qh, kvh,
+                                                hd, length, d);
+        else
+            silvann_gfx950_attention_weights_tq_rows(p, res, (const uint16_t*)q, (const uint8_t*)k, (const uint16_t*)v,
+                                                     qh, kvh, hd, length, d, rows);
+        save(d_dir(d) + "/p.bin", p, rows * qh * length * 4);
+        save(d_dir(d) + "/res_w.bin", res, rows * qh * rf * 4);
+        if (std::string(mode) == "tq")
+            silvann_gfx950_attention_residual_mix_tq(res, p, (const uint8_t*)k, (const uint16_t*)v, qh, kvh, hd, length, d);
+        else
+            silvann_gfx950_attention_residual_mix_tq_rows(res, p, (const uint8_t*)k, (const uint16_t*)v, qh, kvh, hd, length,
+                                                          d, rows);
+        save(d_dir(d) + "/res.bin", res, rows * qh * rf * 4);
+        save(d_dir(d) + "/over.bin", over, 4);
+        fprintf(stderr, "emu done: refused %d, wave exchanges %ld\n", silvann::emu_refused, (long)emu::ops);
+        return silvann::emu_refused ? 5 : 0;
     } else {                               // a0 = most, a1 = rows
         char* lens = load(d + "/lens.bin", "lens");
         on = a1 * qh * hd * 2;

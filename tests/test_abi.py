@@ -69,16 +69,16 @@ def _fn_addr(L, name):
 
 
 def test_install_writes_the_rows_a_table_reaches():
-    """silvann_gfx950_attention_install: the 17 reference rows land at their indices in a table of the
+    """silvann_gfx950_attention_install: the reference rows land at their indices in a table of the
     reference's size (the two appended rows do not fit it and are not written); a table grown by two rows
-    takes all 19; every other slot is left as it was; NULL answers 0."""
+    takes them too; every other slot is left as it was; NULL answers 0."""
     if not _lib.LIB_PATH.exists():
         pytest.skip("library not built")
     from oracle.oracle import ROWS, NN_ROWS
     L = _lib.lib()
     text = _lib.HEADER.read_text()
     rows = {int(i): n for n, i in re.findall(r"#define SILVANN_GFX950_ROW_(\w+) (\d+)u", text)}
-    for nslots, expect in ((NN_ROWS, 17), (NN_ROWS + 2, 19)):
+    for nslots, expect in ((NN_ROWS, len(ROWS)), (NN_ROWS + 2, len(ROWS) + 2)):
         buf = (ctypes.c_uint64 * (1 + nslots))()
         sentinel = 0x5A5A0000
         for i in range(nslots):
@@ -90,19 +90,20 @@ def test_install_writes_the_rows_a_table_reaches():
                 assert buf[1 + i] == _fn_addr(L, "silvann_gfx950_" + rows[i].lower()), rows[i]
             else:
                 assert buf[1 + i] == sentinel + i, i
-    assert len([i for i in rows if i < NN_ROWS]) == len(ROWS) == 17
+    assert len([i for i in rows if i < NN_ROWS]) == len(ROWS) == 21
     assert L.silvann_gfx950_attention_install(None) == 0
 
 
 def test_install_into_a_copy_of_the_reference_table(ref):
-    """Over a copy of the x86_avx2 family's own nn table (oracle/_ref): our 17 rows replace the family's,
+    """Over a copy of the x86_avx2 family's own nn table (oracle/_ref): our rows replace the family's,
     every other door pointer is the family's own."""
     L = _lib.lib()
     nn = ref.family.package_doors[1]
     size = ctypes.c_uint32.from_address(nn).value
     copy = (ctypes.c_uint8 * size)()
     ctypes.memmove(copy, nn, size)
-    assert L.silvann_gfx950_attention_install(ctypes.addressof(copy)) == 17
+    from oracle.oracle import ROWS
+    assert L.silvann_gfx950_attention_install(ctypes.addressof(copy)) == len(ROWS)
     mine = (ctypes.c_uint64 * ((size - 8) // 8)).from_address(ctypes.addressof(copy) + 8)
     theirs = (ctypes.c_uint64 * ((size - 8) // 8)).from_address(nn + 8)
     text = _lib.HEADER.read_text()

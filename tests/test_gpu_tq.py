@@ -1,0 +1,67 @@
+"""TurboQuant rows on gfx950 (gpu.cuh:163-164, 197-198) against the C oracle, through the C ABI.
+
+The same shapes and bars as the emulated kernel tests in tests/test_tq.py: weights within 1e-4 relative,
+the residual's {m, l} within 1e-5 relative and its acc within 1e-4 relative, and the finished fp16 answer at
+max-abs <= 2e-3, cos >= 0.9999.
+"""
+import numpy as np
+import pytest
+import torch
+
+from silvann_amd import doors
+from tests.conftest import parity
+from tests.gpu_util import t
+from tests.test_tq import header_levels, make
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.mark.parametrize("d,hd,qh,kvh,length,rows", [
+    (8, 128, 8, 2, 300, 0),
+    (4, 256, 16, 2, 2500, 0),
+    (3, 100, 6, 3, 50, 0),
+    (8, 320, 2, 1, 64, 0),
+    (4, 64, 4, 2, 2100, 3),
+    (8, 128, 16, 2, 70000, 0),   # a long cold tier: many splits
+])
+def test_tq_doors(dev, oracle, d, hd, qh, kvh, length, rows):
+    rng = np.random.default_rng(d + hd + length)
+    lev = header_levels(d)
+    n = max(rows, 1)
+    q, codes, scales = make(rng, qh, kvh, hd, length, d, rows=n)
+    print(f"case: tq d{d} hd{hd} qh{qh} kvh{kvh} length{length} rows{rows}", flush=True)
+    p = torch.zeros(n * qh * length, dtype=torch.float32, device=dev)
+    res = torch.full((n * qh * (hd + 2),), float("nan"), dtype=torch.float32, device=dev)
+    qd, cd, sd = t(q, dev), t(codes, dev), t(scales, dev)
+    if rows:
+        doors.attention_weights_tq_rows(p, res, qd, cd, sd, qh, kvh, hd, length, d, rows)
+        po, ro = oracle.weights_tq_rows(q, codes, scales, qh, kvh, hd, length, d, n, lev)
+    else:
+        doors.attention_weights_tq(p, res, qd, cd, sd, qh, kvh, hd, length, d)
+        po, ro = oracle.weights_tq(q, codes, scales, qh, kvh, hd, length, d, lev)
+    w = hd + 2
+    np.testing.assert_allclose(p.cpu().numpy(), po, rtol=1e-4, atol=1e-6)
+    np.testing.assert_allclose(res.cpu().numpy().reshape(-1, w)[:, :2], ro.reshape(-1, w)[:, :2], rtol=1e-5)
+    if rows:
+        doors.attention_residual_mix_tq_rows(res, p, cd, sd, qh, kvh, hd, length, d, rows)
+        ro2 = oracle.residual_mix_tq_rows(ro, po, codes, scales, qh, kvh, hd, length, d, n, lev)
+    else:
+        doors.attention_residual_mix_tq(res, p, cd, sd, qh, kvh, hd, length, d)
+        ro2 = oracle.residual_mix_tq(ro, po, codes, scales, qh, kvh, hd, length, d, lev)
+    got = res.cpu().numpy()
+    np.testing.assert_allclose(got.reshape(-1, w)[:, 2:], ro2.reshape(-1, w)[:, 2:], rtol=1e-4,
+                               atol=1e-5 * float(np.abs(ro2).max()))
+    fin = lambda r: (r.reshape(-1, w)[:, 2:] / r.reshape(-1, w)[:, 1:2]).astype(np.float16)  # noqa: E731
+    parity(fin(got), fin(ro2))
+    assert not doors.launch_failed()
+
+
+def test_tq_refuses_unknown_width(dev):
+    p = torch.zeros(64, dtype=torch.float32, device=dev)
+    res = torch.zeros(2 * 66, dtype=torch.float32, device=dev)
+    q = torch.zeros(2 * 64, dtype=torch.float16, device=dev)
+    codes = torch.zeros(64, dtype=torch.uint8, device=dev)
+    scales = torch.zeros(4, dtype=torch.float16, device=dev)
+    doors.launch_failed()
+    doors.attention_weights_tq(p, res, q, codes, scales, 2, 1, 64, 1, 6)
+    assert doors.launch_failed()

@@ -76,3 +76,22 @@ def test_paged_checks():
     refuses(FAULT_BOUNDS, verbs.causal_paged, q, kv, kv, pages, o, qh, kvh, hd, (1 << 31) - 1, 2, page_size=32)
     refuses(FAULT_BOUNDS, verbs.causal_paged, q, kv, kv, None, o, qh, kvh, hd, 0, 2)          # cache too small
     refuses(FAULT_BOUNDS, verbs.causal_paged, q, kv, kv, None, o, 6, 4, hd, 0, 2)             # 6 % 4
+
+
+def test_residual_tq_checks():
+    """attention__abi.cuh:245-266: width 4 or 8 and whole groups (OPCT), then every operand's room (NPBN)."""
+    qh, kvh, hd, d, n = 8, 2, 64, 4, 10
+    rb = verbs.tq_row_bytes(d, hd)
+    codes = lambda b: torch.zeros(b, dtype=torch.uint8)  # noqa: E731
+    q, kc, ks, vc, vs = h(qh * hd), codes(n * kvh * rb), h(n * kvh), codes(n * kvh * rb), h(n * kvh)
+    s, r = f(qh * n), f(qh * (hd + 2))
+    args = (q, kc, ks, vc, vs, s, r)
+    refuses(FAULT_TYPE, verbs.residual_tq, *args, qh, kvh, hd, 3, n)          # a width the tiers do not use
+    refuses(FAULT_TYPE, verbs.residual_tq, *args, 6, 4, hd, d, n)             # 6 % 4
+    refuses(FAULT_TYPE, verbs.residual_tq, *args, qh, kvh, hd, d, 0)          # no rows
+    refuses(FAULT_BOUNDS, verbs.residual_tq, h(qh * hd - 1), kc, ks, vc, vs, s, r, qh, kvh, hd, d, n)
+    refuses(FAULT_BOUNDS, verbs.residual_tq, q, kc, h(n * kvh - 1), vc, vs, s, r, qh, kvh, hd, d, n)
+    refuses(FAULT_BOUNDS, verbs.residual_tq, q, kc, ks, vc, vs, f(qh * n - 1), r, qh, kvh, hd, d, n)
+    refuses(FAULT_BOUNDS, verbs.residual_tq, q, kc, ks, vc, vs, s, f(qh * (hd + 2) - 1), qh, kvh, hd, d, n)
+    # the codes' bytes against their room in halves, as the reference compares them
+    refuses(FAULT_BOUNDS, verbs.residual_tq, q, codes(n * kvh * rb // 2 - 2), ks, vc, vs, s, r, qh, kvh, hd, d, n)
