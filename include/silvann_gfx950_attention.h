@@ -172,6 +172,22 @@ void silvann_gfx950_attention_causal_paged(uint16_t* o, const uint16_t* q, const
                                            uint64_t kv_heads, uint64_t head_dim, uint64_t first, uint64_t rows,
                                            unsigned int* over);
 
+/* The TurboQuant residual in one pass: what `attention_weights_tq` + `attention_residual_mix_tq` (gpu.cuh:163-164)
+ * leave in `res`, for `rows` query rows over the same `length` TurboQuant key and value rows — row u's q_heads at
+ * q + u·q_heads·head_dim, its residuals at res + u·q_heads·(head_dim + 2) — as `attention_weights_tq_rows` +
+ * `attention_residual_mix_tq_rows` (gpu.cuh:197-198) give them. Codes as in row 69; d is 4 or 8 (the tiers' widths,
+ * attention__abi.cuh:258); head_dim 64, 128 or 256; the code planes 8-byte aligned; other operands are refused.
+ * Split-K on MFMA: no weights are materialised and every code is read once. `scratch` holds the splits' residuals,
+ * `silvann_gfx950_attention_residual_tq_scratch` bytes. The tiers' verbs call weights_tq then residual_mix_tq then
+ * merge (mixer__abi.cuh:395-410); this row replaces the first two. */
+#define SILVANN_GFX950_ROW_ATTENTION_RESIDUAL_TQ 139u
+void silvann_gfx950_attention_residual_tq(float* res, const uint16_t* q, const uint8_t* k_codes,
+                                          const uint16_t* k_scales, const uint8_t* v_codes, const uint16_t* v_scales,
+                                          uint64_t q_heads, uint64_t kv_heads, uint64_t head_dim, uint64_t length,
+                                          uint64_t d, uint64_t rows, float* scratch);
+uint64_t silvann_gfx950_attention_residual_tq_scratch(uint64_t q_heads, uint64_t kv_heads, uint64_t head_dim,
+                                                      uint64_t length, uint64_t d, uint64_t rows);
+
 /* Puts this library's rows into an nn door table: `nn_doors` is the reference's `nn__doors` (a uint32 `size`
  * in bytes, then one function pointer a row from byte 8, gpu.cuh:93-241; entry.cuh:33-45 fills it). Every row
  * above whose index the table's size reaches is overwritten with this library's door, as a family's

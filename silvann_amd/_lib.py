@@ -42,6 +42,8 @@ SIGNATURES = {
                                               _p, _p],
     "silvann_gfx950_attention_decode_paged_scratch": [_u64, _u64, _u64, _u64, _u64],
     "silvann_gfx950_attention_causal_paged": [_p, _p, _p, _p, _p, _u64, _u64, _u64, _u64, _u64, _u64, _p],
+    "silvann_gfx950_attention_residual_tq": [_p, _p, _p, _p, _p, _p, _u64, _u64, _u64, _u64, _u64, _u64, _p],
+    "silvann_gfx950_attention_residual_tq_scratch": [_u64, _u64, _u64, _u64, _u64, _u64],
     "silvann_gfx950_set_stream": [_p],
     "silvann_gfx950_get_stream": [],
     "silvann_gfx950_launch_failed": [],
@@ -52,6 +54,7 @@ SIGNATURES = {
 }
 RESTYPES = {
     "silvann_gfx950_attention_decode_paged_scratch": _u64,
+    "silvann_gfx950_attention_residual_tq_scratch": _u64,
     "silvann_gfx950_get_stream": _p,
     "silvann_gfx950_launch_failed": C.c_int,
     "silvann_gfx950_profile_read": C.c_int,

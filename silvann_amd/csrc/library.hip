@@ -146,6 +146,7 @@ SILVANN_EXPORT uint32_t silvann_gfx950_attention_install(void* nn_doors) {
         {SILVANN_GFX950_ROW_ATTENTION_MIX_ROWS, (void*)&silvann_gfx950_attention_mix_rows},
         {SILVANN_GFX950_ROW_ATTENTION_DECODE_PAGED, (void*)&silvann_gfx950_attention_decode_paged},
         {SILVANN_GFX950_ROW_ATTENTION_CAUSAL_PAGED, (void*)&silvann_gfx950_attention_causal_paged},
+        {SILVANN_GFX950_ROW_ATTENTION_RESIDUAL_TQ, (void*)&silvann_gfx950_attention_residual_tq},
     };
     uint32_t size;
     memcpy(&size, nn_doors, sizeof size);

@@ -123,6 +123,32 @@ def residual_tq(q, k_codes, k_scales, v_codes, v_scales, scores, res, q_heads, k
     return res
 
 
+def residual_tq_scratch_bytes(q_heads, kv_heads, head_dim, count, d, rows=1) -> int:
+    return int(doors.attention_residual_tq_scratch(q_heads, kv_heads, head_dim, count, d, rows))
+
+
+def residual_tq_fused(q, k_codes, k_scales, v_codes, v_scales, res, scratch, q_heads, kv_heads, head_dim, d, count,
+                      rows=1):
+    """`residual_tq`'s answer through the fused row (attention_residual_tq): the same operand checks
+    (attention__abi.cuh:245-266), no weights materialised, `rows` query rows over the same keys (the tiered
+    prefill window, prefill__abi.cuh:437-440). `scratch` holds residual_tq_scratch_bytes(...) bytes."""
+    q_heads, kv_heads, head_dim = _dim(q_heads), _dim(kv_heads), _dim(head_dim)
+    d, count, rows = _dim(d), _dim(count), _dim(rows)
+    if d not in (4, 8) or q_heads % kv_heads or head_dim not in (64, 128, 256):
+        raise Fault(FAULT_TYPE)
+    n = count * kv_heads
+    code_bytes = n * tq_row_bytes(d, head_dim)
+    if (not _fits(rows * q_heads * head_dim, room(q)) or code_bytes > room(k_codes) or not _fits(n, room(k_scales))
+            or code_bytes > room(v_codes) or not _fits(n, room(v_scales))
+            or not _fits(2 * rows * q_heads * (head_dim + 2), room(res))
+            or scratch.numel() * scratch.element_size()
+            < residual_tq_scratch_bytes(q_heads, kv_heads, head_dim, count, d, rows)):
+        raise Fault(FAULT_BOUNDS)
+    doors.attention_residual_tq(res, q, k_codes, k_scales, v_codes, v_scales, q_heads, kv_heads, head_dim, count, d,
+                                rows, scratch)
+    return res
+
+
 def merge(a, b, into, q_heads, head_dim):
     """`(nn__attention__merge a b into q_heads head_dim)` — attention__abi.cuh:212-227."""
     q_heads, head_dim = _dim(q_heads), _dim(head_dim)

@@ -19,7 +19,7 @@ import numpy as np
 
 HERE = Path(__file__).resolve().parent
 BUILD = HERE / "_build"
-SOURCES = ["prefill.hip", "decode.hip", "doors.hip"]
+SOURCES = ["prefill.hip", "decode.hip", "doors.hip", "tq_decode.hip"]
 CXX_CANDIDATES = ["/opt/rocm/llvm/bin/clang++", "/opt/rocm/lib/llvm/bin/clang++", shutil.which("clang++") or ""]
 FLAGS = ["-std=c++20", "-O1", "-g", "-fno-omit-frame-pointer", "-rdynamic", "-w", "-pthread"]
 
@@ -102,3 +102,10 @@ def run_tq(q, codes, scales, qh, kvh, hd, length, d, rows=0, timeout: int = 900)
     params = f"{'tq_rows' if rows else 'tq'} {qh} {kvh} {hd} {length} {max(rows, 1)} {d} 0 0"
     return _run({"q": q, "k": codes, "v": scales}, params, None, timeout,
                 outs=(("p", np.float32), ("res_w", np.float32), ("res", np.float32)))
+
+
+def run_tq_fused(q, k_codes, k_scales, v_codes, v_scales, qh, kvh, hd, length, d, rows=1, timeout: int = 900):
+    """attention_residual_tq: the residual of `rows` query rows over the TurboQuant keys and values."""
+    params = f"tq_fused {qh} {kvh} {hd} {length} {rows} {d} 0 0"
+    return _run({"q": q, "k": k_codes, "v": v_codes, "pages": k_scales, "lens": v_scales}, params, None, timeout,
+                outs=(("res", np.float32),))

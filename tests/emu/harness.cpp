@@ -105,6 +105,23 @@ int main(int argc, char** argv) {
         memset(o, 0, on);
         silvann_gfx950_attention_causal_paged((uint16_t*)o, (const uint16_t*)q, (const uint16_t*)k, (const uint16_t*)v,
                                               (const uint32_t*)pages, ps, qh, kvh, hd, a0, a1, over);
+    } else if (std::string(mode) == "tq_fused") {
+        // a0 = length, a1 = rows, ps = d; k / v the codes, pages / lens the key / value scales
+        const unsigned long length = a0, rows = a1, d = ps, rf = hd + 2;
+        char* ksc = pages;
+        char* vsc = load(d_dir(0) + "/lens.bin", "v_scales");
+        float* res = (float*)guarded(rows * qh * rf * 4, "res");
+        memset(res, 0xFF, rows * qh * rf * 4);
+        const uint64_t sb = silvann_gfx950_attention_residual_tq_scratch(qh, kvh, hd, length, d, rows);
+        float* scratch = (float*)guarded(sb ? sb : 4, "scratch");
+        memset(scratch, 0xFF, sb ? sb : 4);
+        silvann_gfx950_attention_residual_tq(res, (const uint16_t*)q, (const uint8_t*)k, (const uint16_t*)ksc,
+                                             (const uint8_t*)v, (const uint16_t*)vsc, qh, kvh, hd, length, d, rows,
+                                             scratch);
+        save(d_dir(0) + "/res.bin", res, rows * qh * rf * 4);
+        save(d_dir(0) + "/over.bin", over, 4);
+        fprintf(stderr, "emu done: refused %d, wave exchanges %ld\n", silvann::emu_refused, (long)emu::ops);
+        return silvann::emu_refused ? 5 : 0;
     } else if (std::string(mode) == "tq" || std::string(mode) == "tq_rows") {
         // a0 = length, a1 = rows, ps = d; k holds the codes, v the scales
         const unsigned long length = a0, rows = a1, d = ps, rf = hd + 2;

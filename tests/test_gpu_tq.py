@@ -65,3 +65,35 @@ def test_tq_refuses_unknown_width(dev):
     doors.launch_failed()
     doors.attention_weights_tq(p, res, q, codes, scales, 2, 1, 64, 1, 6)
     assert doors.launch_failed()
+
+
+@pytest.mark.parametrize("d,hd,qh,kvh,length,rows", [
+    (4, 128, 8, 2, 300, 1),
+    (8, 256, 16, 2, 700, 1),
+    (4, 64, 4, 4, 130, 3),
+    (8, 128, 32, 2, 64, 1),
+    (4, 128, 16, 2, 100000, 1),   # a long cold tier
+])
+def test_fused_residual(dev, oracle, d, hd, qh, kvh, length, rows):
+    """attention_residual_tq (row 139) against weights_tq_rows + residual_mix_tq_rows in the oracle, the
+    residual compared at the oracle's m (a residual is {m, l, acc} up to a common e^m), the answer at the bar."""
+    from silvann_amd import verbs
+    rng = np.random.default_rng(d * 5 + hd + length)
+    lev = header_levels(d)
+    q, kc, ks = make(rng, qh, kvh, hd, length, d, rows=rows)
+    _, vc, vs = make(rng, qh, kvh, hd, length, d)
+    print(f"case: tq fused d{d} hd{hd} qh{qh} kvh{kvh} length{length} rows{rows}", flush=True)
+    res = torch.full((rows * qh * (hd + 2),), float("nan"), dtype=torch.float32, device=dev)
+    scratch = torch.empty(verbs.residual_tq_scratch_bytes(qh, kvh, hd, length, d, rows), dtype=torch.uint8, device=dev)
+    verbs.residual_tq_fused(t(q, dev), t(kc, dev), t(ks, dev), t(vc, dev), t(vs, dev), res, scratch, qh, kvh, hd, d,
+                            length, rows)
+    po, ro = oracle.weights_tq_rows(q, kc, ks, qh, kvh, hd, length, d, rows, lev)
+    ro = oracle.residual_mix_tq_rows(ro, po, vc, vs, qh, kvh, hd, length, d, rows, lev)
+    w = hd + 2
+    got, want = res.cpu().numpy().reshape(-1, w).astype(np.float64), ro.reshape(-1, w).astype(np.float64)
+    np.testing.assert_allclose(got[:, 0], want[:, 0], rtol=0, atol=2e-3 * max(1.0, float(np.abs(want[:, 0]).max())))
+    at = np.exp(got[:, 0] - want[:, 0])[:, None]
+    np.testing.assert_allclose(got[:, 1:2] * at, want[:, 1:2], rtol=2e-3)
+    fin = lambda r: (r[:, 2:] / r[:, 1:2]).astype(np.float16)  # noqa: E731
+    parity(fin(got), fin(want))
+    assert not doors.launch_failed()

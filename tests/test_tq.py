@@ -137,3 +137,35 @@ def test_emulated_kernels(oracle, d, hd, qh, kvh, length, rows):
     # the finished answer, as attention_finish gives it: acc / l in fp16
     fin = lambda r: (r.reshape(-1, w)[:, 2:] / r.reshape(-1, w)[:, 1:2]).astype(np.float16)  # noqa: E731
     parity(fin(res), fin(ro2))
+
+
+# ── the fused row (attention_residual_tq, row 139) in the CPU emulation ──────────────────────────────────
+
+@pytest.mark.parametrize("d,hd,qh,kvh,length,rows", [
+    (4, 128, 8, 2, 300, 1),      # the cold tier's width, one decode query
+    (8, 256, 16, 2, 700, 1),     # the warm tier's width, several splits
+    (4, 64, 4, 4, 130, 3),       # group 1, three query rows (the tiered prefill window)
+    (8, 128, 32, 2, 64, 1),      # a group of 16: one full head block
+])
+def test_emulated_fused_residual(oracle, d, hd, qh, kvh, length, rows):
+    from tests.emu import emu
+    if emu.compiler() is None:
+        pytest.skip("no clang++ for the CPU emulation")
+    rng = np.random.default_rng(d * 5 + hd + length)
+    lev = header_levels(d)
+    q, kc, ks = make(rng, qh, kvh, hd, length, d, rows=rows)
+    _, vc, vs = make(rng, qh, kvh, hd, length, d)
+    res, over, _ = emu.run_tq_fused(q, kc, ks, vc, vs, qh, kvh, hd, length, d, rows=rows)
+    po, ro = oracle.weights_tq_rows(q, kc, ks, qh, kvh, hd, length, d, rows, lev)
+    ro = oracle.residual_mix_tq_rows(ro, po, vc, vs, qh, kvh, hd, length, d, rows, lev)
+    w = hd + 2
+    got, want = res.reshape(-1, w).astype(np.float64), ro.reshape(-1, w).astype(np.float64)
+    # m is the largest score: the keys go through the matrix cores as fp16 (level · scale rounded), so within
+    # that rounding. A residual is {m, l, acc} up to a common factor e^m (attention_merge takes any), so l and acc
+    # are compared at the reference's m.
+    np.testing.assert_allclose(got[:, 0], want[:, 0], rtol=0, atol=2e-3 * max(1.0, float(np.abs(want[:, 0]).max())))
+    at = np.exp(got[:, 0] - want[:, 0])[:, None]
+    np.testing.assert_allclose(got[:, 1:2] * at, want[:, 1:2], rtol=2e-3)
+    np.testing.assert_allclose(got[:, 2:] * at, want[:, 2:], rtol=0, atol=4e-3 * float(np.abs(want[:, 2:]).max()))
+    fin = lambda r: (r[:, 2:] / r[:, 1:2]).astype(np.float16)  # noqa: E731
+    parity(fin(got), fin(want))
