@@ -14,7 +14,8 @@ launch moves per rocprofv3 FETCH_SIZE + WRITE_SIZE, read from profiles/traffic.j
 measurement of this kernel and workload (else null).
 
 `secondary` holds the other configurations' lines (decode GB/s for C1 and C5; prefill TFLOP/s for C3 and
-C4 against 2.5 PFLOP/s dense fp16), each timed the same way.
+C4 against 2.5 PFLOP/s dense fp16), each timed the same way, then the fused TurboQuant residual
+(attention_residual_tq) over a 4-bit and an 8-bit tier of C5's shape, in GB/s of codes, scales, q and residuals.
 
 `cpu_baseline` is the reference's own x86_avx2 silicon family (oracle/_ref, built from the reference's
 sources) over the same batch, its doors called through its nn table on the host cores — both of the
@@ -49,7 +50,8 @@ def parse():
     ap.add_argument("--no-secondary", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-threads", type=int, default=int(os.environ.get("BENCH_CPU_THREADS", "16")))
-    ap.add_argument("--only", type=int, default=0, help="time only this config (1-5), no CPU leg")
+    ap.add_argument("--only", type=int, default=0,
+                    help="time only this config (1-5: BASELINE.json's; 6, 7: a 4-bit / 8-bit TurboQuant tier), no CPU leg")
     ap.add_argument("--copy-probe", action="store_true",
                     help="run a plain 1 GiB device-to-device copy 5 times and exit: the known-size kernel the "
                          "FETCH_SIZE / WRITE_SIZE counters are scaled by")
@@ -75,7 +77,7 @@ def time_steps(step, steps, warmup, kernel):
         step()
     torch.cuda.synchronize()
     L.silvann_gfx950_profile_enable(1)
-    for k in ("decode_split", "decode_merge", "causal_mfma"):
+    for k in ("decode_split", "decode_merge", "causal_mfma", "tq_split"):
         prof_read(k)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
@@ -85,7 +87,7 @@ def time_steps(step, steps, warmup, kernel):
     wall = time.perf_counter() - t0
     L.silvann_gfx950_profile_enable(0)
     kms, n = prof_read(kernel)
-    others = {k: prof_read(k) for k in ("decode_split", "decode_merge", "causal_mfma") if k != kernel}
+    others = {k: prof_read(k) for k in ("decode_split", "decode_merge", "causal_mfma", "tq_split") if k != kernel}
     if silvann_amd.doors.launch_failed():
         raise RuntimeError("a launch failed during the timed steps")
     return wall, kms / max(n, 1), others
@@ -156,6 +158,26 @@ def bench_causal(w, dev, steps, warmup):
     }, out
 
 
+def bench_tier(w, dev, steps, warmup):
+    """The fused TurboQuant residual (attention_residual_tq) over one tier: GB/s of codes, scales, q and residuals."""
+    import torch
+    from silvann_amd import doors, verbs
+    res = torch.zeros(w.rows * w.q_heads * (w.head_dim + 2), dtype=torch.float32, device=dev)
+    scratch = torch.empty(max(verbs.residual_tq_scratch_bytes(w.q_heads, w.kv_heads, w.head_dim, w.length, w.d, w.rows), 4),
+                          dtype=torch.uint8, device=dev)
+
+    def step():
+        doors.attention_residual_tq(res, w.q, w.k_codes, w.k_scales, w.v_codes, w.v_scales, w.q_heads, w.kv_heads,
+                                    w.head_dim, w.length, w.d, w.rows, scratch)
+    wall, kms, _ = time_steps(step, steps, warmup, "tq_split")
+    b = w.io_bytes()
+    return {
+        "config": w.name, "unit": "GB/s", "value": b * steps / wall / 1e9, "ms_per_step": wall / steps * 1e3,
+        "bytes_per_step": b, "split_ms": kms, "kernel_gbs": b / (kms * 1e-3) / 1e9,
+        "frac": b / (kms * 1e-3) / 1e9 / HBM_PEAK_GBS,
+    }, res
+
+
 def cpu_baseline(w, threads):
     """The reference x86_avx2 family over the whole C2 batch (both decode routes, the faster reported); the C
     restatement on one core as "port" where oracle/_ref is absent."""
@@ -224,6 +246,10 @@ def main():
         print(json.dumps({"copy_probe_bytes": src.numel() * 2, "launches": 5}), flush=True)
         return
 
+    if a.only in W.TIERS:
+        r = bench_tier(W.TIERS[a.only](dev=dev), dev, a.steps, a.warmup)[0]
+        print(json.dumps(r), flush=True)
+        return
     if a.only:
         w = W.CONFIGS[a.only](dev=dev)
         r = (bench_decode if a.only in (1, 2, 5) else bench_causal)(w, dev, a.steps, a.warmup)[0]
@@ -241,6 +267,10 @@ def main():
         for n in (3, 4):
             w = W.CONFIGS[n](dev=dev)
             secondary.append(bench_causal(w, dev, max(3, a.steps // 4), min(a.warmup, 2))[0])
+            del w
+        for n in sorted(W.TIERS):
+            w = W.TIERS[n](dev=dev)
+            secondary.append(bench_tier(w, dev, max(5, a.steps // 2), a.warmup)[0])
             del w
         torch.cuda.empty_cache()
     cpu = None if a.no_cpu else cpu_baseline(w2, a.cpu_threads)

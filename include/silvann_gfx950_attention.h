@@ -207,7 +207,7 @@ void* silvann_gfx950_get_stream(void);
  * device answers false, amd_rocm_base/sys.cuh:39-62 and amd_rocm_base/nn.cuh:29-33). */
 int silvann_gfx950_launch_failed(void);
 /* Live kernel timing: with profiling on, this thread's doors bracket their main kernels with hipEvents on
- * their stream. `kernel` is "decode_split", "decode_merge" or "causal_mfma"; read synchronises, answers the
+ * their stream. `kernel` is "decode_split", "decode_merge", "causal_mfma" or "tq_split"; read synchronises, answers the
  * summed milliseconds and the launch count since the last read, and clears them. Answers -1 for an unknown
  * name or a failed event. */
 void silvann_gfx950_profile_enable(int on);

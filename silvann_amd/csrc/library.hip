@@ -84,7 +84,7 @@ SILVANN_EXPORT int silvann_gfx950_launch_failed(void) {
     return silvann::failed[d].exchange(0);
 }
 static int prof_index(const char* kernel) {
-    static const char* names[silvann::kProfKernels] = {"decode_split", "decode_merge", "causal_mfma"};
+    static const char* names[silvann::kProfKernels] = {"decode_split", "decode_merge", "causal_mfma", "tq_split"};
     for (int i = 0; i < silvann::kProfKernels; ++i)
         if (kernel && strcmp(kernel, names[i]) == 0) return i;
     return -1;

@@ -312,6 +312,7 @@ void residual_tq_launch(float* res, const uint16_t* q, const uint8_t* kc, const 
     a.part = scratch;
     hipStream_t st = stream();
     const dim3 mgrid((uint32_t)q_heads, (uint32_t)rows, (uint32_t)(head_dim / 64));
+    prof_begin(kProfTqSplit);
     if (a.nsplit > 0) {
         const dim3 grid(a.nsplit * a.kv_heads * a.hblocks * a.rows);
 #define SILVANN_TQ(HDV, DV) \
@@ -319,6 +320,7 @@ void residual_tq_launch(float* res, const uint16_t* q, const uint8_t* kc, const 
         SILVANN_TQ(64, 4) SILVANN_TQ(64, 8) SILVANN_TQ(128, 4) SILVANN_TQ(128, 8) SILVANN_TQ(256, 4) SILVANN_TQ(256, 8)
 #undef SILVANN_TQ
     }
+    prof_end(kProfTqSplit);
     switch (head_dim) {
         case 64: tq_merge<64><<<mgrid, 256, 0, st>>>(res, scratch, a.q_heads, a.nsplit); break;
         case 128: tq_merge<128><<<mgrid, 256, 0, st>>>(res, scratch, a.q_heads, a.nsplit); break;

@@ -183,3 +183,69 @@ def config5(seed=5, dev=None) -> Decode:
 
 
 CONFIGS = {1: config1, 2: config2, 3: config3, 4: config4, 5: config5}
+
+
+@dataclass
+class Tier:
+    """A TurboQuant tier of one layer's cache (the tiers' verbs, mixer__abi.cuh:395-410): `length` key and value
+    rows of width d (8 warm, 4 cold), kv head g of position t at row t·kv_heads + g, and `rows` rotated queries."""
+    name: str
+    q_heads: int
+    kv_heads: int
+    head_dim: int
+    length: int
+    d: int
+    rows: int
+    q: object
+    k_codes: object
+    k_scales: object
+    v_codes: object
+    v_scales: object
+    seed: int = 0
+
+    def row_bytes(self) -> int:
+        per = 16 // self.d
+        return (self.head_dim + per - 1) // per * 2
+
+    def io_bytes(self) -> int:
+        """What one pass reads and writes: every key and value row (codes and scale) once, the queries and the
+        residuals."""
+        cache = self.length * self.kv_heads * 2 * (self.row_bytes() + 2)
+        return cache + self.rows * self.q_heads * (self.head_dim * 2 + (self.head_dim + 2) * 4)
+
+
+def tier(name, q_heads, kv_heads, head_dim, length, d, rows=1, seed=0, dev=None) -> Tier:
+    """Codes uniform over every code, scales the codec's for unit-rms rows (fp16(clip_d), kernels.cuh:2905-2925),
+    q N(0,1) — the rows a rotated Gaussian cache encodes to, without running the encoder."""
+    clip = {4: 2.7325895709952577, 8: 4.6036453045214065}[d]
+    per = 16 // d
+    rb = (head_dim + per - 1) // per * 2
+    n = length * kv_heads
+    if dev is None:
+        rng = np.random.default_rng(seed)
+        q = _normal(rng, rows * q_heads * head_dim)
+        kc = rng.integers(0, 256, n * rb, dtype=np.uint8)
+        vc = rng.integers(0, 256, n * rb, dtype=np.uint8)
+        sc = np.full(n, clip, np.float16).view(np.uint16)
+        return Tier(name, q_heads, kv_heads, head_dim, length, d, rows, q, kc, sc.copy(), vc, sc.copy(), seed)
+    import torch
+    g = torch.Generator(device=dev)
+    g.manual_seed(seed)
+    q = device_normal(rows * q_heads * head_dim, 3 * seed + 1, dev)
+    kc = torch.randint(0, 256, (n * rb,), generator=g, dtype=torch.uint8, device=dev)
+    vc = torch.randint(0, 256, (n * rb,), generator=g, dtype=torch.uint8, device=dev)
+    sc = torch.full((n,), clip, dtype=torch.float16, device=dev)
+    return Tier(name, q_heads, kv_heads, head_dim, length, d, rows, q, kc, sc, vc, sc.clone(), seed)
+
+
+def tier_cold(seed=6, dev=None) -> Tier:
+    """A long cold tier at C5's shape: 262,144 positions of 4-bit rows, 16 q / 2 kv heads, head_dim 256."""
+    return tier("tq4_16q2kv_hd256_len262144", 16, 2, 256, 262144, 4, seed=seed, dev=dev)
+
+
+def tier_warm(seed=7, dev=None) -> Tier:
+    """The same at the warm tier's 8 bits."""
+    return tier("tq8_16q2kv_hd256_len262144", 16, 2, 256, 262144, 8, seed=seed, dev=dev)
+
+
+TIERS = {6: tier_cold, 7: tier_warm}
