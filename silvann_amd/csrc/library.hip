@@ -162,5 +162,5 @@ SILVANN_EXPORT uint32_t silvann_gfx950_attention_install(void* nn_doors) {
 }
 
 SILVANN_EXPORT const char* silvann_gfx950_version(void) {
-    return "gfx950 decode-splitk-mfma16 causal-mfma32 doors-17 v1";
+    return "gfx950 decode-splitk-mfma16 causal-mfma32 tq-mfma16 doors-24 v1";
 }
