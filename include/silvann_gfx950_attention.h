@@ -172,6 +172,18 @@ void silvann_gfx950_attention_causal_paged(uint16_t* o, const uint16_t* q, const
                                            uint64_t kv_heads, uint64_t head_dim, uint64_t first, uint64_t rows,
                                            unsigned int* over);
 
+/* The causal residual of row 138: what `attention_weights_rows` + `attention_residual_mix_rows` (gpu.cuh:195-196;
+ * doors.cuh:201-204,417-432, a row at a time) leave in `res` with `first` — row r's q_heads at
+ * q + r·q_heads·head_dim over positions 0 .. first + r, its residuals {m, l, acc[head_dim]} at
+ * res + r·q_heads·(head_dim + 2) — over a paged or contiguous cache as row 138 takes it. The tiered prefill
+ * window's part (prefill__abi.cuh:420-435, part 0) in one MFMA launch and without the weights. m is the row's
+ * largest scaled score. Shapes as row 138; other operands (and a NULL res) are refused. */
+#define SILVANN_GFX950_ROW_ATTENTION_CAUSAL_RESIDUAL_PAGED 140u
+void silvann_gfx950_attention_causal_residual_paged(float* res, const uint16_t* q, const uint16_t* k,
+                                                    const uint16_t* v, const uint32_t* pages, uint64_t page_size,
+                                                    uint64_t q_heads, uint64_t kv_heads, uint64_t head_dim,
+                                                    uint64_t first, uint64_t rows);
+
 /* The TurboQuant residual in one pass: what `attention_weights_tq` + `attention_residual_mix_tq` (gpu.cuh:163-164)
  * leave in `res`, for `rows` query rows over the same `length` TurboQuant key and value rows — row u's q_heads at
  * q + u·q_heads·head_dim, its residuals at res + u·q_heads·(head_dim + 2) — as `attention_weights_tq_rows` +

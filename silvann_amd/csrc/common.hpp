@@ -20,6 +20,7 @@ typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 // packages/nn/contracts/objects/primitives.cuh:57, kernels.cuh:29-40).
 constexpr unsigned int kFaultOverflow = 0x4E504F56u;
 constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kLn2 = 0.6931471805599453f;
 
 // fp32 -> fp16 with round-to-nearest-even, subnormals kept: the hardware conversion gives the bits of the
 // reference's hand-written one (kernels.cuh:2763-2808) for every finite input. A finite input whose answer

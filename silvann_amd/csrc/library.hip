@@ -147,6 +147,7 @@ SILVANN_EXPORT uint32_t silvann_gfx950_attention_install(void* nn_doors) {
         {SILVANN_GFX950_ROW_ATTENTION_DECODE_PAGED, (void*)&silvann_gfx950_attention_decode_paged},
         {SILVANN_GFX950_ROW_ATTENTION_CAUSAL_PAGED, (void*)&silvann_gfx950_attention_causal_paged},
         {SILVANN_GFX950_ROW_ATTENTION_RESIDUAL_TQ, (void*)&silvann_gfx950_attention_residual_tq},
+        {SILVANN_GFX950_ROW_ATTENTION_CAUSAL_RESIDUAL_PAGED, (void*)&silvann_gfx950_attention_causal_residual_paged},
     };
     uint32_t size;
     memcpy(&size, nn_doors, sizeof size);
@@ -162,5 +163,5 @@ SILVANN_EXPORT uint32_t silvann_gfx950_attention_install(void* nn_doors) {
 }
 
 SILVANN_EXPORT const char* silvann_gfx950_version(void) {
-    return "gfx950 decode-splitk-mfma16 causal-mfma32 tq-mfma16 doors-24 v1";
+    return "gfx950 decode-splitk-mfma16 causal-mfma32 tq-mfma16 doors-25 v1";
 }

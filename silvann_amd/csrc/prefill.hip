@@ -56,6 +56,7 @@ struct CausalArgs {
     uint32_t first, rows;   // first + rows < 2^31: positions and key counts are 32-bit
     float scale_log2;   // 1/sqrt(head_dim) · log2(e)
     unsigned int* over;
+    float* res;         // the residual form: row r, head h at res + (r·q_heads + h)·(head_dim + 2)
 };
 
 // Tile chunk swizzles (16-byte chunks, CPR of them a row). K: the S^T A-operand read takes one chunk from
@@ -112,7 +113,10 @@ __device__ __forceinline__ void scale_acc(float& x, float c) {
 }
 
 // PTL: the page table fits LDS (kPagesInLds entries) and tiles look their page up there.
-template <int HD, bool PAIRED, bool PTL>
+// RES: write each row's residual {m, l, acc} (the reference's `attention_weights` + `attention_residual_mix`
+// contract, kernels.cuh:1186-1238: m the row's largest scaled score, l = Σ e^(s − m), acc = Σ e^(s − m)·v)
+// instead of its fp16 answer.
+template <int HD, bool PAIRED, bool PTL, bool RES = false>
 __global__ __launch_bounds__(kThreads) void causal_mfma(CausalArgs a) {
     constexpr int CPR = HD / 8;        // 16-byte chunks in a key row
     constexpr int KSTEPS = HD / 16;    // k-steps of S^T (16 dims each)
@@ -208,6 +212,7 @@ __global__ __launch_bounds__(kThreads) void causal_mfma(CausalArgs a) {
 #pragma unroll
         for (int n = 0; n < DT; ++n) acc[n] = (f32x16)0.0f;
         float m = -INFINITY, l = 0.0f;
+        float mt = -INFINITY;   // RES: the row's true running max (m lags it by up to kRescale)
 
         // The load cursor: tiles are loaded in order, so the page and the offset in it advance by a tile
         // each load (page_size is a multiple of the tile).
@@ -319,6 +324,7 @@ __global__ __launch_bounds__(kThreads) void causal_mfma(CausalArgs a) {
         // only when some lane needs it (always on the first tile, rarely after), in place on the matrix
         // cores' accumulator registers, so the accumulator keeps one register assignment through the loop.
         auto rescale = [&]() __attribute__((always_inline)) {
+            if constexpr (RES) mt = fmaxf(mt, mx);
             if (__builtin_amdgcn_ballot_w64(mx > m + kRescale)) {
                 const float mnew = fmaxf(m, mx);
                 const float corr = __builtin_amdgcn_exp2f(m - mnew);
@@ -426,6 +432,21 @@ __global__ __launch_bounds__(kThreads) void causal_mfma(CausalArgs a) {
 
         l += __shfl_xor(l, 32);
         if (!row_ok) return;
+        if constexpr (RES) {
+            // against the true max: every weight 2^(s·scale − mt) <= 1, and m in the scores' own units
+            const float corr = __builtin_amdgcn_exp2f(m - mt);
+            float* rrow = a.res + ((uint64_t)myrow * a.q_heads + head) * (HD + 2);
+            if (half == 0) *(float2*)rrow = make_float2(mt * kLn2, l * corr);
+#pragma unroll
+            for (int n = 0; n < DT; ++n)
+#pragma unroll
+                for (int qd = 0; qd < 4; ++qd) {
+                    float* at = rrow + 2 + 32 * n + 8 * qd + 4 * half;
+                    *(float2*)at = make_float2(acc[n][4 * qd] * corr, acc[n][4 * qd + 1] * corr);
+                    *(float2*)(at + 2) = make_float2(acc[n][4 * qd + 2] * corr, acc[n][4 * qd + 3] * corr);
+                }
+            return;
+        }
         const float inv_l = 1.0f / l;
         uint16_t* orow = a.o + ((uint64_t)myrow * a.q_heads + head) * HD;
 #pragma unroll
@@ -797,18 +818,19 @@ static bool prefill_pipe() {
     return on;
 }
 
-void causal_paged_launch(uint16_t* o, const uint16_t* q, const uint16_t* k, const uint16_t* v, const uint32_t* pages,
-                         uint64_t page_size, uint64_t q_heads, uint64_t kv_heads, uint64_t head_dim, uint64_t first,
-                         uint64_t rows, unsigned int* over) {
+// o (with over) for the fp16 answers, or res for the residuals; what = the entry point's name
+void causal_paged_launch(uint16_t* o, float* res, const uint16_t* q, const uint16_t* k, const uint16_t* v,
+                         const uint32_t* pages, uint64_t page_size, uint64_t q_heads, uint64_t kv_heads,
+                         uint64_t head_dim, uint64_t first, uint64_t rows, unsigned int* over, const char* what) {
     const bool ok = (head_dim == 64 || head_dim == 128 || head_dim == 256) && kv_heads > 0 && q_heads % kv_heads == 0 &&
                     rows > 0 && first + rows < (1ull << 31) &&
                     (!pages || (page_size > 0 && page_size < (1ull << 31) && page_size % kKT == 0));
     if (!ok) {
-        refuse("attention_causal_paged");
+        refuse(what);
         return;
     }
     CausalArgs a;
-    a.o = o; a.q = q; a.k = k; a.v = v; a.pages = pages; a.page_size = (uint32_t)page_size;
+    a.o = o; a.res = res; a.q = q; a.k = k; a.v = v; a.pages = pages; a.page_size = (uint32_t)page_size;
     a.q_heads = (uint32_t)q_heads; a.kv_heads = (uint32_t)kv_heads; a.group = (uint32_t)(q_heads / kv_heads);
     a.hw = a.group % 4 == 0 ? 4 : (a.group % 2 == 0 ? 2 : 1);
     a.hblocks = a.group / a.hw;
@@ -823,6 +845,14 @@ void causal_paged_launch(uint16_t* o, const uint16_t* q, const uint16_t* k, cons
     hipStream_t st = stream();
     prof_begin(kProfCausal);
     const bool ptl = pages && (first + rows + page_size - 1) / page_size <= kPagesInLds;
+#define SILVANN_CAUSAL_RES(HDV) \
+    if (paired) { \
+        if (ptl) causal_mfma<HDV, true, true, true><<<grid, kThreads, 0, st>>>(a); \
+        else causal_mfma<HDV, true, false, true><<<grid, kThreads, 0, st>>>(a); \
+    } else { \
+        if (ptl) causal_mfma<HDV, false, true, true><<<grid, kThreads, 0, st>>>(a); \
+        else causal_mfma<HDV, false, false, true><<<grid, kThreads, 0, st>>>(a); \
+    }
 #define SILVANN_CAUSAL(HDV) \
     if (paired) { \
         if (ptl) causal_mfma<HDV, true, true><<<grid, kThreads, 0, st>>>(a); \
@@ -831,7 +861,13 @@ void causal_paged_launch(uint16_t* o, const uint16_t* q, const uint16_t* k, cons
         if (ptl) causal_mfma<HDV, false, true><<<grid, kThreads, 0, st>>>(a); \
         else causal_mfma<HDV, false, false><<<grid, kThreads, 0, st>>>(a); \
     }
-    switch (head_dim) {
+    if (res) {
+        switch (head_dim) {
+            case 64: SILVANN_CAUSAL_RES(64) break;
+            case 128: SILVANN_CAUSAL_RES(128) break;
+            default: SILVANN_CAUSAL_RES(256) break;
+        }
+    } else switch (head_dim) {
         case 64: SILVANN_CAUSAL(64) break;
         case 128: SILVANN_CAUSAL(128) break;
         default:
@@ -849,8 +885,9 @@ void causal_paged_launch(uint16_t* o, const uint16_t* q, const uint16_t* k, cons
             break;
     }
 #undef SILVANN_CAUSAL
+#undef SILVANN_CAUSAL_RES
     prof_end(kProfCausal);
-    check_launch("attention_causal_paged");
+    check_launch(what);
 }
 
 }  // namespace silvann
@@ -859,5 +896,19 @@ SILVANN_EXPORT void silvann_gfx950_attention_causal_paged(uint16_t* o, const uin
                                                           const uint16_t* v, const uint32_t* pages, uint64_t page_size,
                                                           uint64_t q_heads, uint64_t kv_heads, uint64_t head_dim,
                                                           uint64_t first, uint64_t rows, unsigned int* over) {
-    silvann::causal_paged_launch(o, q, k, v, pages, page_size, q_heads, kv_heads, head_dim, first, rows, over);
+    silvann::causal_paged_launch(o, nullptr, q, k, v, pages, page_size, q_heads, kv_heads, head_dim, first, rows, over,
+                                 "attention_causal_paged");
+}
+
+SILVANN_EXPORT void silvann_gfx950_attention_causal_residual_paged(float* res, const uint16_t* q, const uint16_t* k,
+                                                                   const uint16_t* v, const uint32_t* pages,
+                                                                   uint64_t page_size, uint64_t q_heads,
+                                                                   uint64_t kv_heads, uint64_t head_dim, uint64_t first,
+                                                                   uint64_t rows) {
+    if (!res) {
+        silvann::refuse("attention_causal_residual_paged");
+        return;
+    }
+    silvann::causal_paged_launch(nullptr, res, q, k, v, pages, page_size, q_heads, kv_heads, head_dim, first, rows,
+                                 nullptr, "attention_causal_residual_paged");
 }

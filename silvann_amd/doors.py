@@ -53,6 +53,7 @@ attention_mix_rows = _door("attention_mix_rows")
 attention_decode_paged = _door("attention_decode_paged")
 attention_decode_paged_scratch = _door("attention_decode_paged_scratch")
 attention_causal_paged = _door("attention_causal_paged")
+attention_causal_residual_paged = _door("attention_causal_residual_paged")
 attention_residual_tq = _door("attention_residual_tq")
 attention_residual_tq_scratch = _door("attention_residual_tq_scratch")
 

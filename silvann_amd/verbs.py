@@ -244,3 +244,152 @@ def causal_paged(q, k, v, pages, out, q_heads, kv_heads, head_dim, first, rows, 
         over = torch.zeros(1, dtype=torch.int32, device=q.device)
     doors.attention_causal_paged(out, q, k, v, pages, page_size, q_heads, kv_heads, head_dim, first, rows, over)
     return out
+
+
+def causal_residual_paged(q, k, v, pages, res, q_heads, kv_heads, head_dim, first, rows, page_size=0):
+    """The residuals {m, l, acc} of positions first .. first+rows-1 over the (paged) cache, row r's at
+    res + r·q_heads·(head_dim + 2) — what weights_rows + residual_mix_rows leave (doors.cuh:201-204,417-432),
+    in one launch of the fused MFMA door (row 140). The same checks as causal_paged."""
+    q_heads, kv_heads, head_dim = _dim(q_heads), _dim(kv_heads), _dim(head_dim)
+    if (not isinstance(first, int) or first < 0 or not isinstance(rows, int) or rows <= 0 or q_heads % kv_heads
+            or head_dim not in (64, 128, 256)):
+        raise Fault(FAULT_BOUNDS)
+    qw, kvw, to = q_heads * head_dim, kv_heads * head_dim, first + rows
+    if to >= 1 << 31 or not _fits(rows * qw, room(q)) or not _fits(2 * rows * q_heads * (head_dim + 2), room(res)):
+        raise Fault(FAULT_BOUNDS)
+    if pages is None:
+        if not _fits(to * kvw, room(k)) or not _fits(to * kvw, room(v)):
+            raise Fault(FAULT_BOUNDS)
+    elif page_size <= 0 or page_size % 32 or (to + page_size - 1) // page_size > pages.numel():
+        raise Fault(FAULT_BOUNDS)
+    doors.attention_causal_residual_paged(res, q, k, v, pages, page_size, q_heads, kv_heads, head_dim, first, rows)
+    return res
+
+
+# ── the tiered prefill window (ai_qwen_3 prefill__abi.cuh:409-447, step ④) ─────────────────────────────────
+
+WARM_BITS, COLD_BITS = 8, 4   # prefill__abi.cuh:433: the warm tier's codes are 8 bits, the cold tier's 4
+
+
+def _tier_ok(tier, kv_heads, head_dim, d) -> bool:
+    if tier is None:
+        return True
+    kc, ks, vc, vs, count = tier
+    n = count * kv_heads
+    b = n * tq_row_bytes(d, head_dim)
+    return b <= room(kc) and b <= room(vc) and _fits(n, room(ks)) and _fits(n, room(vs))
+
+
+def _window_checks(q, window_k, window_v, first_w, rows, warm, cold, res, att, q_heads, kv_heads, head_dim):
+    q_heads, kv_heads, head_dim = _dim(q_heads), _dim(kv_heads), _dim(head_dim)
+    if not isinstance(first_w, int) or first_w < 0 or not isinstance(rows, int) or rows <= 0 or q_heads % kv_heads:
+        raise Fault(FAULT_TYPE)
+    qw, kvw, window = q_heads * head_dim, kv_heads * head_dim, first_w + rows
+    warm = None if warm is None or warm[4] == 0 else warm
+    cold = None if cold is None or cold[4] == 0 else cold
+    if (not _fits(rows * qw, room(q)) or not _fits(rows * qw, room(att)) or not _fits(window * kvw, room(window_k))
+            or not _fits(window * kvw, room(window_v)) or not _tier_ok(warm, kv_heads, head_dim, WARM_BITS)
+            or not _tier_ok(cold, kv_heads, head_dim, COLD_BITS)
+            or ((warm or cold) and not _fits(2 * 3 * rows * q_heads * (head_dim + 2), room(res)))):
+        raise Fault(FAULT_BOUNDS)
+    return q_heads, kv_heads, head_dim, window, warm, cold
+
+
+def window_attention(q, window_k, window_v, first_w, rows, warm, cold, scores, rows_scores, res, att, q_heads,
+                     kv_heads, head_dim, over):
+    """Step ④ of ai_qwen_3's tiered prefill (prefill__abi.cuh:409-447) as the reference runs it, through the
+    reference's doors: the chunk's `rows` query rows `q` are the last rows of the fp16 window (`first_w` positions
+    before them), contiguous in `window_k` / `window_v`. With no warm or cold rows the chunk attends the window
+    causally (causal_scores_grouped, causal_softmax, causal_mix, 414-418). Past that each row's residual over the
+    window up to its own position (weights_rows + residual_mix_rows), over the whole warm tier (8-bit
+    weights_tq_rows + residual_mix_tq_rows) and over the whole cold tier (4-bit), as many rows a pass as
+    `rows_scores` holds (one row at a time in `scores` when it holds none), merged and finished into `att`.
+    `warm` / `cold` are (k_codes, k_scales, v_codes, v_scales, count) or None; `res` holds three residual blocks of
+    rows·q_heads·(head_dim + 2) floats (r0, r1, r2)."""
+    q_heads, kv_heads, head_dim, window, warm, cold = _window_checks(
+        q, window_k, window_v, first_w, rows, warm, cold, res, att, q_heads, kv_heads, head_dim)
+    qw = q_heads * head_dim
+    if warm is None and cold is None:
+        if rows_scores.numel() * rows_scores.element_size() // 4 < rows * q_heads * window:
+            raise Fault(FAULT_ROOM)
+        doors.attention_causal_scores_grouped(rows_scores, q, window_k, q_heads, kv_heads, head_dim, first_w, rows)
+        doors.attention_causal_softmax(rows_scores, q_heads, first_w, rows)
+        doors.attention_causal_mix(att, rows_scores, window_v, q_heads, kv_heads, head_dim, first_w, rows, over)
+        return att
+    rw = 4 * q_heads * (head_dim + 2)                       # a row's residual, in bytes
+    r0 = res.data_ptr()
+    r1, r2 = r0 + rows * rw, r0 + 2 * rows * rw
+    longest = max(window, warm[4] if warm else 0, cold[4] if cold else 0)
+    if scores.numel() * scores.element_size() // 4 < q_heads * longest:
+        raise Fault(FAULT_ROOM)
+    for part, span, tier, into in ((0, window, None, r0), (1, warm[4] if warm else 0, warm, r1),
+                                   (2, cold[4] if cold else 0, cold, r2)):
+        if span == 0:
+            continue
+        fit = rows_scores.numel() * rows_scores.element_size() // 4 // (q_heads * span)
+        per = 1 if fit == 0 else min(fit, rows)
+        pp = scores if fit == 0 else rows_scores
+        for r in range(0, rows, per):
+            n = min(per, rows - r)
+            qrr = q.data_ptr() + 2 * r * qw
+            if part == 0:
+                doors.attention_weights_rows(pp, into + r * rw, qrr, window_k, q_heads, kv_heads, head_dim, first_w + r,
+                                             n)
+                doors.attention_residual_mix_rows(into + r * rw, pp, window_v, q_heads, kv_heads, head_dim, first_w + r,
+                                                  n)
+            else:
+                kc, ks, vc, vs, _ = tier
+                bits = WARM_BITS if part == 1 else COLD_BITS
+                doors.attention_weights_tq_rows(pp, into + r * rw, qrr, kc, ks, q_heads, kv_heads, head_dim, span, bits,
+                                                n)
+                doors.attention_residual_mix_tq_rows(into + r * rw, pp, vc, vs, q_heads, kv_heads, head_dim, span, bits,
+                                                     n)
+    if warm:
+        doors.attention_merge(r0, r0, r1, rows * q_heads, head_dim)
+    if cold:
+        doors.attention_merge(r0, r0, r2, rows * q_heads, head_dim)
+    doors.attention_finish(att, r0, rows * q_heads, head_dim, over)
+    return att
+
+
+def window_scratch_bytes(q_heads, kv_heads, head_dim, rows, warm_count, cold_count) -> int:
+    """Scratch window_attention_fused needs: the larger of the two tiers' fused-residual scratch (they run one
+    after the other on the stream)."""
+    need = 0
+    for count, d in ((warm_count, WARM_BITS), (cold_count, COLD_BITS)):
+        if count:
+            need = max(need, residual_tq_scratch_bytes(q_heads, kv_heads, head_dim, count, d, rows))
+    return need
+
+
+def window_attention_fused(q, window_k, window_v, first_w, rows, warm, cold, res, scratch, att, q_heads, kv_heads,
+                           head_dim, over):
+    """window_attention's answer through the fused rows: the window part is one causal launch on MFMA (row 138
+    straight into `att` when there are no tiers, else row 140's residuals), each tier one fused TurboQuant
+    residual (row 139) over all the chunk's rows; then the reference's merge and finish. No weights are
+    materialised. head_dim 64, 128 or 256; `scratch` holds window_scratch_bytes(...) bytes."""
+    q_heads, kv_heads, head_dim, window, warm, cold = _window_checks(
+        q, window_k, window_v, first_w, rows, warm, cold, res, att, q_heads, kv_heads, head_dim)
+    if head_dim not in (64, 128, 256) or window >= 1 << 31:
+        raise Fault(FAULT_TYPE)
+    if warm is None and cold is None:
+        doors.attention_causal_paged(att, q, window_k, window_v, None, 0, q_heads, kv_heads, head_dim, first_w, rows,
+                                     over)
+        return att
+    need = window_scratch_bytes(q_heads, kv_heads, head_dim, rows, warm[4] if warm else 0, cold[4] if cold else 0)
+    if scratch is None or scratch.numel() * scratch.element_size() < need:
+        raise Fault(FAULT_BOUNDS)
+    rw = 4 * q_heads * (head_dim + 2)
+    r0 = res.data_ptr()
+    r1, r2 = r0 + rows * rw, r0 + 2 * rows * rw
+    doors.attention_causal_residual_paged(r0, q, window_k, window_v, None, 0, q_heads, kv_heads, head_dim, first_w, rows)
+    for tier, into, bits in ((warm, r1, WARM_BITS), (cold, r2, COLD_BITS)):
+        if tier:
+            kc, ks, vc, vs, count = tier
+            doors.attention_residual_tq(into, q, kc, ks, vc, vs, q_heads, kv_heads, head_dim, count, bits, rows, scratch)
+    if warm:
+        doors.attention_merge(r0, r0, r1, rows * q_heads, head_dim)
+    if cold:
+        doors.attention_merge(r0, r0, r2, rows * q_heads, head_dim)
+    doors.attention_finish(att, r0, rows * q_heads, head_dim, over)
+    return att

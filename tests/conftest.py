@@ -53,3 +53,20 @@ def parity(got, want, atol=2e-3, cos_min=0.9999):
     assert err <= atol, f"max-abs {err:.3e} > {atol}"
     assert cos >= cos_min, f"cosine {cos:.6f} < {cos_min}"
     return err, cos
+
+
+def residual_parity(got, want, hd):
+    """Residuals {m, l, acc} a (row, head) against the oracle's: m (the largest scaled score) to fp32 rounding of
+    the scores, which go through the matrix cores from fp16 operands; l and acc, at the oracle's m (a residual is
+    defined up to a common factor e^m, which attention_merge takes as it comes), to the weights' fp16 rounding;
+    and the answers acc / l to the fp16 bar."""
+    w = hd + 2
+    g, o = got.reshape(-1, w).astype(np.float64), want.reshape(-1, w).astype(np.float64)
+    assert np.all(np.isfinite(g)), "non-finite residual"
+    np.testing.assert_allclose(g[:, 0], o[:, 0], rtol=0, atol=1e-4 * max(1.0, float(np.abs(o[:, 0]).max())))
+    at = np.exp(g[:, 0] - o[:, 0])[:, None]
+    np.testing.assert_allclose(g[:, 1:2] * at, o[:, 1:2], rtol=2e-3)
+    np.testing.assert_allclose(g[:, 2:] * at, o[:, 2:], rtol=0, atol=4e-3 * float(np.abs(o[:, 2:]).max()))
+    fin = lambda r: (r[:, 2:] / r[:, 1:2]).astype(np.float16)  # noqa: E731
+    parity(fin(g), fin(o))
+

@@ -88,6 +88,13 @@ def run_causal(w, env: dict | None = None, timeout: int = 900):
     return _run({"q": w.q, "k": w.k, "v": w.v, "pages": pages}, params, env, timeout)
 
 
+def run_causal_res(w, env: dict | None = None, timeout: int = 900):
+    """attention_causal_residual_paged: the fp32 residuals {m, l, acc} of every row and head."""
+    pages = None if w.pages is None else w.pages.astype(np.uint32)
+    params = f"causal_res {w.q_heads} {w.kv_heads} {w.head_dim} {w.first} {w.rows} {w.page_size} 0 0"
+    return _run({"q": w.q, "k": w.k, "v": w.v, "pages": pages}, params, env, timeout, outs=(("res", np.float32),))
+
+
 def run_decode(w, env: dict | None = None, timeout: int = 900):
     pages = None if w.pages is None else w.pages.astype(np.uint32)
     params = (f"decode {w.q_heads} {w.kv_heads} {w.head_dim} {w.most} {w.rows} {w.page_size} {w.pages_row} "

@@ -24,6 +24,8 @@ inline thread_local EmuDim3 threadIdx, blockIdx;
 inline EmuDim3 blockDim, gridDim;
 struct dim3 { uint32_t x, y, z; dim3(uint32_t a = 1, uint32_t b = 1, uint32_t c = 1) : x(a), y(b), z(c) {} };
 typedef void* hipStream_t;
+struct float2 { float x, y; };
+inline float2 make_float2(float x, float y) { return {x, y}; }
 
 namespace emu {
 constexpr int kScratch = 256;

@@ -1,6 +1,6 @@
-// harness.cpp — TEST INFRASTRUCTURE: runs one call of the library's causal-prefill or paged-decode entry
-// point in the CPU emulation, on inputs and parameters a test wrote to a directory, and writes the answer
-// back there. Every buffer sits against an inaccessible page, so an out-of-bounds read or write stops the
+// harness.cpp — TEST INFRASTRUCTURE: runs one call of one of the library's entry points (causal prefill, its
+// residual form, paged decode, the TurboQuant rows) in the CPU emulation, on inputs and parameters a test
+// wrote to a directory, and writes the answer back there. Every buffer sits against an inaccessible page, so an out-of-bounds read or write stops the
 // run with the buffer, the offset and the lane that made it; a run that outlives its time limit (a lost
 // barrier) stops too.
 #include <execinfo.h>
@@ -105,6 +105,16 @@ int main(int argc, char** argv) {
         memset(o, 0, on);
         silvann_gfx950_attention_causal_paged((uint16_t*)o, (const uint16_t*)q, (const uint16_t*)k, (const uint16_t*)v,
                                               (const uint32_t*)pages, ps, qh, kvh, hd, a0, a1, over);
+    } else if (std::string(mode) == "causal_res") {   // a0 = first, a1 = rows
+        const unsigned long rf = hd + 2;
+        float* res = (float*)guarded(a1 * qh * rf * 4, "res");
+        memset(res, 0xFF, a1 * qh * rf * 4);   // whatever the caller's residual held
+        silvann_gfx950_attention_causal_residual_paged(res, (const uint16_t*)q, (const uint16_t*)k, (const uint16_t*)v,
+                                                       (const uint32_t*)pages, ps, qh, kvh, hd, a0, a1);
+        save(d + "/res.bin", res, a1 * qh * rf * 4);
+        save(d + "/over.bin", over, 4);
+        fprintf(stderr, "emu done: refused %d, wave exchanges %ld\n", silvann::emu_refused, (long)emu::ops);
+        return silvann::emu_refused ? 5 : 0;
     } else if (std::string(mode) == "tq_fused") {
         // a0 = length, a1 = rows, ps = d; k / v the codes, pages / lens the key / value scales
         const unsigned long length = a0, rows = a1, d = ps, rf = hd + 2;

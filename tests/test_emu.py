@@ -14,7 +14,7 @@ import numpy as np
 import pytest
 
 from silvann_amd import workloads as W
-from tests.conftest import parity
+from tests.conftest import parity, residual_parity
 from tests.emu import emu
 
 pytestmark = pytest.mark.skipif(emu.compiler() is None, reason="no clang++ for the CPU emulation")
@@ -58,4 +58,21 @@ def test_decode(oracle, qh, kvh, hd, lens, ps):
     want, _ = oracle.decode_paged(w.q, w.k, w.v, w.pages, w.pages_row, w.page_size, w.k_row, w.lens, qh, kvh, hd,
                                   w.rows)
     parity(got, want)
+    assert over == 0
+
+
+@pytest.mark.parametrize("hd,qh,kvh,first,rows,ps", [
+    (256, 16, 2, 77, 95, 64),    # paged, page table in LDS, the steady loop at head_dim 256
+    (128, 6, 2, 10, 70, 0),      # group 3: one head a wave
+    (64, 8, 2, 300, 40, 32),     # a prefix longer than the chunk: row tiles unpaired
+])
+def test_causal_residual_kernel(oracle, hd, qh, kvh, first, rows, ps):
+    """attention_causal_residual_paged (row 140) against the oracle's attention_weights_rows +
+    attention_residual_mix_rows over the gathered cache, the pair it replaces."""
+    w = W.causal("emu", qh, kvh, hd, first, rows, page_size=ps, seed=hd + rows + 1)
+    got, over, _ = emu.run_causal_res(w)
+    k, v = w.gathered()
+    p, res = oracle.weights_rows(w.q, k, qh, kvh, hd, first, rows)
+    want = oracle.residual_mix_rows(res, p, v, qh, kvh, hd, first, rows)
+    residual_parity(got, want, hd)
     assert over == 0
