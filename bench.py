@@ -15,7 +15,8 @@ measurement of this kernel and workload (else null).
 
 `secondary` holds the other configurations' lines (decode GB/s for C1 and C5; prefill TFLOP/s for C3 and
 C4 against 2.5 PFLOP/s dense fp16), each timed the same way, then the fused TurboQuant residual
-(attention_residual_tq) over a 4-bit and an 8-bit tier of C5's shape, in GB/s of codes, scales, q and residuals.
+(attention_residual_tq) over a 4-bit and an 8-bit tier of C5's shape, in GB/s of codes, scales, q and residuals,
+and the cache writer (attention_cache_write_paged) placing C4's 2,048-row chunk, keys turned, in GB/s.
 
 `cpu_baseline` is the reference's own x86_avx2 silicon family (oracle/_ref, built from the reference's
 sources) over the same batch, its doors called through its nn table on the host cores — both of the
@@ -40,6 +41,7 @@ sys.path.insert(0, str(ROOT))
 HBM_PEAK_GBS = 8000.0
 FP16_PEAK_TFLOPS = 2500.0
 METRIC = "decode-attn GB/s & % HBM peak; prefill-attn TFLOP/s & % MFMA peak"
+KERNELS = ("decode_split", "decode_merge", "causal_mfma", "tq_split", "cache_write")
 
 
 def parse():
@@ -51,7 +53,8 @@ def parse():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-threads", type=int, default=int(os.environ.get("BENCH_CPU_THREADS", "16")))
     ap.add_argument("--only", type=int, default=0,
-                    help="time only this config (1-5: BASELINE.json's; 6, 7: a 4-bit / 8-bit TurboQuant tier), no CPU leg")
+                    help="time only this config (1-5: BASELINE.json's; 6, 7: a 4-bit / 8-bit TurboQuant tier; 8: the "
+                         "cache writer on C4's chunk), no CPU leg")
     ap.add_argument("--copy-probe", action="store_true",
                     help="run a plain 1 GiB device-to-device copy 5 times and exit: the known-size kernel the "
                          "FETCH_SIZE / WRITE_SIZE counters are scaled by")
@@ -77,7 +80,7 @@ def time_steps(step, steps, warmup, kernel):
         step()
     torch.cuda.synchronize()
     L.silvann_gfx950_profile_enable(1)
-    for k in ("decode_split", "decode_merge", "causal_mfma", "tq_split"):
+    for k in KERNELS:
         prof_read(k)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
@@ -87,7 +90,7 @@ def time_steps(step, steps, warmup, kernel):
     wall = time.perf_counter() - t0
     L.silvann_gfx950_profile_enable(0)
     kms, n = prof_read(kernel)
-    others = {k: prof_read(k) for k in ("decode_split", "decode_merge", "causal_mfma", "tq_split") if k != kernel}
+    others = {k: prof_read(k) for k in KERNELS if k != kernel}
     if silvann_amd.doors.launch_failed():
         raise RuntimeError("a launch failed during the timed steps")
     return wall, kms / max(n, 1), others
@@ -178,6 +181,28 @@ def bench_tier(w, dev, steps, warmup):
     }, res
 
 
+def bench_write(w, dev, steps, warmup):
+    """The cache writer (attention_cache_write_paged): a chunk's keys turned and its keys and values placed in
+    their pages, GB/s of rows read and written and angles read."""
+    import torch
+    from silvann_amd import doors
+    over = torch.zeros(1, dtype=torch.int32, device=dev)
+    npr = w.pages.numel()
+
+    def step():
+        doors.attention_cache_write_paged(w.k_cache, w.v_cache, w.pages, npr, w.page_size, w.capacity, w.positions,
+                                          w.rows, w.k, w.v, w.cs, w.rot, w.rows, w.kv_heads, w.head_dim, over)
+    wall, kms, _ = time_steps(step, steps, warmup, "cache_write")
+    if int(over.item()):
+        raise RuntimeError(f"cache writer fault word {int(over.item()):#x}")
+    b = w.io_bytes()
+    return {
+        "config": w.name, "unit": "GB/s", "value": b * steps / wall / 1e9, "ms_per_step": wall / steps * 1e3,
+        "bytes_per_step": b, "kernel_ms": kms, "kernel_gbs": b / (kms * 1e-3) / 1e9,
+        "frac": b / (kms * 1e-3) / 1e9 / HBM_PEAK_GBS,
+    }, None
+
+
 def cpu_baseline(w, threads):
     """The reference x86_avx2 family over the whole C2 batch (both decode routes, the faster reported); the C
     restatement on one core as "port" where oracle/_ref is absent."""
@@ -246,6 +271,10 @@ def main():
         print(json.dumps({"copy_probe_bytes": src.numel() * 2, "launches": 5}), flush=True)
         return
 
+    if a.only in W.WRITES:
+        r = bench_write(W.WRITES[a.only](dev=dev), dev, a.steps, a.warmup)[0]
+        print(json.dumps(r), flush=True)
+        return
     if a.only in W.TIERS:
         r = bench_tier(W.TIERS[a.only](dev=dev), dev, a.steps, a.warmup)[0]
         print(json.dumps(r), flush=True)
@@ -271,6 +300,10 @@ def main():
         for n in sorted(W.TIERS):
             w = W.TIERS[n](dev=dev)
             secondary.append(bench_tier(w, dev, max(5, a.steps // 2), a.warmup)[0])
+            del w
+        for n in sorted(W.WRITES):
+            w = W.WRITES[n](dev=dev)
+            secondary.append(bench_write(w, dev, max(5, a.steps // 2), a.warmup)[0])
             del w
         torch.cuda.empty_cache()
     cpu = None if a.no_cpu else cpu_baseline(w2, a.cpu_threads)

@@ -184,6 +184,25 @@ void silvann_gfx950_attention_causal_residual_paged(float* res, const uint16_t* 
                                                     uint64_t q_heads, uint64_t kv_heads, uint64_t head_dim,
                                                     uint64_t first, uint64_t rows);
 
+/* New key and value rows into their cache slots, the keys turned by RoPE: the reference's `rope_rows` (gpu.cuh:140,
+ * kernels.cuh:1710-1726) pointed at the cache rows, and the value projection's placement, as its rows verb does them
+ * (attention__abi.cuh:398-406; the reference has no writer verb, 13-14 P2) — over a paged cache. Row r (k and v at
+ * + r·kv_heads·head_dim) belongs to sequence u = r / rows_per_seq at position positions[u] + r % rows_per_seq
+ * (`positions` a device array of a uint32 a sequence: a prefill chunk is one sequence of `rows` rows; a decode batch is
+ * `rows` sequences of one row). Its slot is page pages[u·pages_row + position / page_size], offset position %
+ * page_size, of pools laid out as rows 137-138 take them; `pages` NULL: sequence u's cache is contiguous at
+ * u·capacity positions. The key's first `rot` elements are turned by row r's angles at cs + r·rot (rot/2 cosines,
+ * then rot/2 sines; the pairs x[k], x[k + rot/2]): a·c − b·s and b·c + a·s in fp32, rounded to fp16, overflow storing
+ * NPOV in `over`; the rest of the key and the value are copied bit for bit. `cs` NULL: no turn. A row at or past
+ * `capacity` positions is written nowhere and stores NPBN ("NPBN", primitives.cuh:5) in `over`. Refused (nothing
+ * launched): rot odd or past head_dim, pages_row < ⌈capacity / page_size⌉, a NULL operand. */
+#define SILVANN_GFX950_ROW_ATTENTION_CACHE_WRITE_PAGED 141u
+void silvann_gfx950_attention_cache_write_paged(uint16_t* k_cache, uint16_t* v_cache, const uint32_t* pages,
+                                                uint64_t pages_row, uint64_t page_size, uint64_t capacity,
+                                                const uint32_t* positions, uint64_t rows_per_seq, const uint16_t* k,
+                                                const uint16_t* v, const float* cs, uint64_t rot, uint64_t rows,
+                                                uint64_t kv_heads, uint64_t head_dim, unsigned int* over);
+
 /* The TurboQuant residual in one pass: what `attention_weights_tq` + `attention_residual_mix_tq` (gpu.cuh:163-164)
  * leave in `res`, for `rows` query rows over the same `length` TurboQuant key and value rows — row u's q_heads at
  * q + u·q_heads·head_dim, its residuals at res + u·q_heads·(head_dim + 2) — as `attention_weights_tq_rows` +
@@ -219,7 +238,7 @@ void* silvann_gfx950_get_stream(void);
  * device answers false, amd_rocm_base/sys.cuh:39-62 and amd_rocm_base/nn.cuh:29-33). */
 int silvann_gfx950_launch_failed(void);
 /* Live kernel timing: with profiling on, this thread's doors bracket their main kernels with hipEvents on
- * their stream. `kernel` is "decode_split", "decode_merge", "causal_mfma" or "tq_split"; read synchronises, answers the
+ * their stream. `kernel` is "decode_split", "decode_merge", "causal_mfma", "tq_split" or "cache_write"; read synchronises, answers the
  * summed milliseconds and the launch count since the last read, and clears them. Answers -1 for an unknown
  * name or a failed event. */
 void silvann_gfx950_profile_enable(int on);

@@ -5,7 +5,8 @@
  * It follows engine/src/packages/nn/gpu/kernels/kernels.cuh as the reference's host family runs those
  * bodies: one lane of one block (silicon_families/host/nn.cuh:115-162 — lanes()=1, lanes_sum/max the
  * identity), libm expf/sqrtf, every sum serial and in the body's order, no contraction into FMA
- * (built with -ffp-contract=off). Each function names the body it restates.
+ * (built with -ffp-contract=off; oracle_rope_rows writes the reference build's two FMAs out). Each function names
+ * the body it restates.
  *
  * How each function is pinned (tests/test_oracle_*.py):
  *   - against the reference's own x86_avx2 family built from /root/reference (oracle/_ref), bit for bit
@@ -519,4 +520,57 @@ void oracle_attention_causal_rows(uint16_t* o, const uint16_t* q, const uint16_t
         oracle_attention_mix(o + i * q_heads * head_dim, p, vv, q_heads, kv_heads, head_dim, len, over);
     }
     free(p); free(kg); free(vg);
+}
+
+/* kernels.cuh:1710-1726 (`rope_rows`) — each row's heads turned by that row's angles: row r's at cs + r·rot, the rot/2
+ * cosines then the rot/2 sines; of every head (head_stride apart; rows row_stride apart) elements k and k + rot/2,
+ * for k < rot/2, become a·c − b·s and b·c + a·s, rounded to fp16 (overflow to *over). o may be x.
+ * The one place the oracle fuses: the reference family is C++ built without -ffp-contract=off, which GCC then
+ * contracts into fma(a, c, −(b·s)) and fma(b, c, a·s) — found by testing every form against its rope_rows door,
+ * and held to it bit for bit by tests/test_cache.py (the unfused sums differ in the last bit now and then). */
+void oracle_rope_rows(uint16_t* o, const uint16_t* x, const float* cs, uint64_t rows, uint64_t heads,
+                      uint64_t head_stride, uint64_t row_stride, uint64_t rot, uint32_t* over) {
+    const uint64_t pairs = rot / 2u;
+    for (uint64_t r = 0; r < rows; ++r)
+        for (uint64_t e = 0; e < heads; ++e)
+            for (uint64_t k = 0; k < pairs; ++k) {
+                const uint64_t at = r * row_stride + e * head_stride + k;
+                const float a = h2f(x[at]), b = h2f(x[at + pairs]);
+                const float c = cs[r * rot + k], s = cs[r * rot + pairs + k];
+                int hit = 0;
+                o[at] = oracle_float_to_half(fmaf(a, c, -(b * s)), &hit);
+                if (hit) *over = FAULT_OVERFLOW;
+                hit = 0;
+                o[at + pairs] = oracle_float_to_half(fmaf(b, c, a * s), &hit);
+                if (hit) *over = FAULT_OVERFLOW;
+            }
+}
+
+/* The page-aware cache writer (no reference counterpart: the reference's rows verb turns the chunk's keys with
+ * rope_rows straight into the contiguous cache and places the values there, attention__abi.cuh:398-406). Row r of
+ * k / v belongs to sequence u = r / rows_per_seq at position positions[u] + r % rows_per_seq; its slot is page
+ * pages[u·pages_row + position / page_size] at offset position % page_size (pages NULL: u·capacity + position). The
+ * key is copied there and its first rot elements turned in place by oracle_rope_rows with row r's angles (cs NULL:
+ * not turned); the value is copied. A position at or past capacity writes nothing and stores "NPBN", which
+ * outranks an overflow: NPOV goes into *over only when no row was out of bounds and *over was clear. */
+void oracle_attention_cache_write_paged(uint16_t* kc, uint16_t* vc, const uint32_t* pages, uint64_t pages_row,
+                                        uint64_t page_size, uint64_t capacity, const uint32_t* positions,
+                                        uint64_t rows_per_seq, const uint16_t* k, const uint16_t* v, const float* cs,
+                                        uint64_t rot, uint64_t rows, uint64_t kv_heads, uint64_t head_dim,
+                                        uint32_t* over) {
+    const uint64_t row = kv_heads * head_dim;
+    uint32_t turned = 0;
+    int out = 0;
+    for (uint64_t r = 0; r < rows; ++r) {
+        const uint64_t u = r / rows_per_seq, p = (uint64_t)positions[u] + r % rows_per_seq;
+        if (p >= capacity) { out = 1; continue; }
+        const uint64_t slot = pages ? (uint64_t)pages[u * pages_row + p / page_size] * page_size + p % page_size
+                                    : u * capacity + p;
+        memcpy(kc + slot * row, k + r * row, row * sizeof(uint16_t));
+        memcpy(vc + slot * row, v + r * row, row * sizeof(uint16_t));
+        if (cs && rot)
+            oracle_rope_rows(kc + slot * row, kc + slot * row, cs + r * rot, 1u, kv_heads, head_dim, row, rot, &turned);
+    }
+    if (out) *over = 0x4E50424Eu;   /* "NPBN", contracts/objects/primitives.cuh:5 */
+    else if (turned && *over == 0) *over = turned;
 }

@@ -43,6 +43,8 @@ SIGNATURES = {
     "silvann_gfx950_attention_decode_paged_scratch": [_u64, _u64, _u64, _u64, _u64],
     "silvann_gfx950_attention_causal_paged": [_p, _p, _p, _p, _p, _u64, _u64, _u64, _u64, _u64, _u64, _p],
     "silvann_gfx950_attention_causal_residual_paged": [_p, _p, _p, _p, _p, _u64, _u64, _u64, _u64, _u64, _u64],
+    "silvann_gfx950_attention_cache_write_paged": [_p, _p, _p, _u64, _u64, _u64, _p, _u64, _p, _p, _p, _u64, _u64,
+                                                   _u64, _u64, _p],
     "silvann_gfx950_attention_residual_tq": [_p, _p, _p, _p, _p, _p, _u64, _u64, _u64, _u64, _u64, _u64, _p],
     "silvann_gfx950_attention_residual_tq_scratch": [_u64, _u64, _u64, _u64, _u64, _u64],
     "silvann_gfx950_set_stream": [_p],

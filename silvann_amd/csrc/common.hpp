@@ -92,7 +92,8 @@ void check_launch(const char* what);
 // with hipEvents on its stream; silvann_gfx950_profile_read sums them.
 void prof_begin(int kernel);
 void prof_end(int kernel);
-enum ProfKernel : int { kProfDecodeSplit = 0, kProfDecodeMerge = 1, kProfCausal = 2, kProfTqSplit = 3, kProfKernels = 4 };
+enum ProfKernel : int { kProfDecodeSplit = 0, kProfDecodeMerge = 1, kProfCausal = 2, kProfTqSplit = 3, kProfCacheWrite = 4,
+                       kProfKernels = 5 };
 // Records a door that refused its operands without launching (printed, remembered the same way).
 void refuse(const char* what);
 

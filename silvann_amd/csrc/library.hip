@@ -84,7 +84,8 @@ SILVANN_EXPORT int silvann_gfx950_launch_failed(void) {
     return silvann::failed[d].exchange(0);
 }
 static int prof_index(const char* kernel) {
-    static const char* names[silvann::kProfKernels] = {"decode_split", "decode_merge", "causal_mfma", "tq_split"};
+    static const char* names[silvann::kProfKernels] = {"decode_split", "decode_merge", "causal_mfma", "tq_split",
+                                                              "cache_write"};
     for (int i = 0; i < silvann::kProfKernels; ++i)
         if (kernel && strcmp(kernel, names[i]) == 0) return i;
     return -1;
@@ -148,6 +149,7 @@ SILVANN_EXPORT uint32_t silvann_gfx950_attention_install(void* nn_doors) {
         {SILVANN_GFX950_ROW_ATTENTION_CAUSAL_PAGED, (void*)&silvann_gfx950_attention_causal_paged},
         {SILVANN_GFX950_ROW_ATTENTION_RESIDUAL_TQ, (void*)&silvann_gfx950_attention_residual_tq},
         {SILVANN_GFX950_ROW_ATTENTION_CAUSAL_RESIDUAL_PAGED, (void*)&silvann_gfx950_attention_causal_residual_paged},
+        {SILVANN_GFX950_ROW_ATTENTION_CACHE_WRITE_PAGED, (void*)&silvann_gfx950_attention_cache_write_paged},
     };
     uint32_t size;
     memcpy(&size, nn_doors, sizeof size);
@@ -163,5 +165,5 @@ SILVANN_EXPORT uint32_t silvann_gfx950_attention_install(void* nn_doors) {
 }
 
 SILVANN_EXPORT const char* silvann_gfx950_version(void) {
-    return "gfx950 decode-splitk-mfma16 causal-mfma32 tq-mfma16 doors-25 v1";
+    return "gfx950 decode-splitk-mfma16 causal-mfma32 tq-mfma16 cache-writer doors-26 v1";
 }

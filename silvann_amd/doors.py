@@ -55,6 +55,7 @@ attention_decode_paged_scratch = _door("attention_decode_paged_scratch")
 attention_causal_paged = _door("attention_causal_paged")
 attention_causal_residual_paged = _door("attention_causal_residual_paged")
 attention_residual_tq = _door("attention_residual_tq")
+attention_cache_write_paged = _door("attention_cache_write_paged")
 attention_residual_tq_scratch = _door("attention_residual_tq_scratch")
 
 

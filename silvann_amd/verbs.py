@@ -393,3 +393,37 @@ def window_attention_fused(q, window_k, window_v, first_w, rows, warm, cold, res
         doors.attention_merge(r0, r0, r2, rows * q_heads, head_dim)
     doors.attention_finish(att, r0, rows * q_heads, head_dim, over)
     return att
+
+
+# ── the page-aware cache writer ──────────────────────────────────────────────────────────────────────────
+
+
+def cache_write_paged(k_cache, v_cache, pages, positions, k, v, cs, kv_heads, head_dim, rows, rows_per_seq,
+                      capacity, page_size=0, pages_row=0, rot=None, over=None):
+    """New key and value rows into their slots (row 141): what the reference's rows verb does with `rope_rows`
+    pointed at the contiguous cache and the value projection's placement (attention__abi.cuh:398-406), over a paged
+    cache. `positions` a uint32 GPU tensor, a sequence's first new position each; `cs` the rows' angles (rot/2
+    cosines then rot/2 sines a row, fp32) or None; `rot` defaults to head_dim. A row at or past `capacity` leaves
+    NPBN in the fault word (check_fault raises it)."""
+    kv_heads, head_dim, rows, rows_per_seq = _dim(kv_heads), _dim(head_dim), _dim(rows), _dim(rows_per_seq)
+    if not isinstance(capacity, int) or capacity <= 0 or capacity >= 1 << 32:
+        raise Fault(FAULT_BOUNDS)
+    rot = head_dim if rot is None else rot
+    if cs is not None and (rot % 2 or rot > head_dim or rot <= 0):
+        raise Fault(FAULT_TYPE)
+    row = kv_heads * head_dim
+    nseq = (rows + rows_per_seq - 1) // rows_per_seq
+    if (not _fits(rows * row, room(k)) or not _fits(rows * row, room(v)) or positions.numel() < nseq
+            or (cs is not None and cs.numel() < rows * rot)):
+        raise Fault(FAULT_BOUNDS)
+    if pages is None:
+        if not _fits(nseq * capacity * row, room(k_cache)) or not _fits(nseq * capacity * row, room(v_cache)):
+            raise Fault(FAULT_BOUNDS)
+    elif (page_size <= 0 or pages_row < (capacity + page_size - 1) // page_size
+          or pages.numel() < (nseq - 1) * pages_row + (capacity + page_size - 1) // page_size):
+        raise Fault(FAULT_BOUNDS)
+    if over is None:
+        over = torch.zeros(1, dtype=torch.int32, device=k.device)
+    doors.attention_cache_write_paged(k_cache, v_cache, pages, pages_row, page_size, capacity, positions, rows_per_seq,
+                                      k, v, cs, rot if cs is not None else 0, rows, kv_heads, head_dim, over)
+    return over

@@ -249,3 +249,62 @@ def tier_warm(seed=7, dev=None) -> Tier:
 
 
 TIERS = {6: tier_cold, 7: tier_warm}
+
+
+@dataclass
+class Write:
+    """New rows for the cache writer (attention_cache_write_paged): `rows` key and value rows of one sequence at
+    positions first .. first+rows-1, the keys turned over `rot` elements by their positions' angles, into
+    permuted pages of a pool sized for first + rows positions."""
+    name: str
+    kv_heads: int
+    head_dim: int
+    first: int
+    rows: int
+    page_size: int
+    rot: int
+    pages: object
+    positions: object
+    k: object
+    v: object
+    cs: object
+    k_cache: object
+    v_cache: object
+    seed: int = 0
+
+    @property
+    def capacity(self) -> int:
+        return self.first + self.rows
+
+    def io_bytes(self) -> int:
+        """What one write moves: each new key and value row read and written once, and the angles read."""
+        return self.rows * self.kv_heads * self.head_dim * 2 * 2 * 2 + self.rows * self.rot * 4
+
+
+def write(name, kv_heads, head_dim, first, rows, page_size, rot=None, seed=0, dev=None) -> Write:
+    import torch
+    rot = head_dim if rot is None else rot
+    rng = np.random.default_rng(seed)
+    npages = (first + rows + page_size - 1) // page_size
+    pages = rng.permutation(npages).astype(np.int32)
+    i = np.arange(rot // 2, dtype=np.float64)
+    ang = np.arange(first, first + rows, dtype=np.float64)[:, None] * 1e6 ** (-2.0 * i / rot)[None, :]
+    cs = np.concatenate([np.cos(ang), np.sin(ang)], axis=1).astype(np.float32).ravel()
+    n = rows * kv_heads * head_dim
+    k = device_normal(n, 5 * seed + 1, dev)
+    v = device_normal(n, 5 * seed + 2, dev)
+    slots = npages * page_size * kv_heads * head_dim
+    kc = torch.zeros(slots, dtype=torch.float16, device=dev)
+    vc = torch.zeros(slots, dtype=torch.float16, device=dev)
+    t = lambda a: torch.from_numpy(a).to(dev)  # noqa: E731
+    return Write(name, kv_heads, head_dim, first, rows, page_size, rot, t(pages), t(np.array([first], np.int32)), k, v,
+                 t(cs), kc, vc, seed)
+
+
+def write_c4(seed=8, dev=None) -> Write:
+    """C4's chunk written before it is attended: 2,048 rows after a 100,000-position prefix, 2 kv heads, head_dim
+    256, fully turned, into 256-position permuted pages."""
+    return write("write_2kv_hd256_rows2048_at100000", 2, 256, 100000, 2048, 256, seed=seed, dev=dev)
+
+
+WRITES = {8: write_c4}

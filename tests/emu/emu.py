@@ -19,7 +19,7 @@ import numpy as np
 
 HERE = Path(__file__).resolve().parent
 BUILD = HERE / "_build"
-SOURCES = ["prefill.hip", "decode.hip", "doors.hip", "tq_decode.hip"]
+SOURCES = ["prefill.hip", "decode.hip", "doors.hip", "tq_decode.hip", "cache.hip"]
 CXX_CANDIDATES = ["/opt/rocm/llvm/bin/clang++", "/opt/rocm/lib/llvm/bin/clang++", shutil.which("clang++") or ""]
 FLAGS = ["-std=c++20", "-O1", "-g", "-fno-omit-frame-pointer", "-rdynamic", "-w", "-pthread"]
 
@@ -116,3 +116,12 @@ def run_tq_fused(q, k_codes, k_scales, v_codes, v_scales, qh, kvh, hd, length, d
     params = f"tq_fused {qh} {kvh} {hd} {length} {rows} {d} 0 0"
     return _run({"q": q, "k": k_codes, "v": v_codes, "pages": k_scales, "lens": v_scales}, params, None, timeout,
                 outs=(("res", np.float32),))
+
+
+def run_cache_write(kc, vc, pages, pages_row, page_size, capacity, positions, rows_per_seq, k, v, cs, rot, rows, kvh,
+                    hd, timeout: int = 900):
+    """attention_cache_write_paged over copies of the caches `kc` / `vc`: the caches after it, and the fault word."""
+    pages = None if pages is None else np.ascontiguousarray(pages, np.uint32)
+    params = f"cache {rot} {kvh} {hd} {rows_per_seq} {rows} {page_size} {pages_row} {capacity}"
+    return _run({"q": cs, "k": k, "v": v, "pages": pages, "lens": np.ascontiguousarray(positions, np.uint32),
+                 "kc": kc, "vc": vc}, params, None, timeout, outs=(("kc_out", np.uint16), ("vc_out", np.uint16)))

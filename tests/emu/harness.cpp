@@ -1,5 +1,5 @@
 // harness.cpp — TEST INFRASTRUCTURE: runs one call of one of the library's entry points (causal prefill, its
-// residual form, paged decode, the TurboQuant rows) in the CPU emulation, on inputs and parameters a test
+// residual form, paged decode, the TurboQuant rows, the cache writer) in the CPU emulation, on inputs and parameters a test
 // wrote to a directory, and writes the answer back there. Every buffer sits against an inaccessible page, so an out-of-bounds read or write stops the
 // run with the buffer, the offset and the lane that made it; a run that outlives its time limit (a lost
 // barrier) stops too.
@@ -105,6 +105,21 @@ int main(int argc, char** argv) {
         memset(o, 0, on);
         silvann_gfx950_attention_causal_paged((uint16_t*)o, (const uint16_t*)q, (const uint16_t*)k, (const uint16_t*)v,
                                               (const uint32_t*)pages, ps, qh, kvh, hd, a0, a1, over);
+    } else if (std::string(mode) == "cache") {
+        // qh = rot, a0 = rows_per_seq, a1 = rows, k_row = capacity; q holds the angles (fp32), lens the positions,
+        // kc / vc the caches as they were
+        size_t kn = 0, vn = 0;
+        char* kc = load(d + "/kc.bin", "k_cache", &kn);
+        char* vc = load(d + "/vc.bin", "v_cache", &vn);
+        char* lens = load(d + "/lens.bin", "positions");
+        silvann_gfx950_attention_cache_write_paged((uint16_t*)kc, (uint16_t*)vc, (const uint32_t*)pages, pages_row, ps,
+                                                   k_row, (const uint32_t*)lens, a0, (const uint16_t*)k,
+                                                   (const uint16_t*)v, (const float*)q, qh, a1, kvh, hd, over);
+        save(d + "/kc_out.bin", kc, kn);
+        save(d + "/vc_out.bin", vc, vn);
+        save(d + "/over.bin", over, 4);
+        fprintf(stderr, "emu done: refused %d, wave exchanges %ld\n", silvann::emu_refused, (long)emu::ops);
+        return silvann::emu_refused ? 5 : 0;
     } else if (std::string(mode) == "causal_res") {   // a0 = first, a1 = rows
         const unsigned long rf = hd + 2;
         float* res = (float*)guarded(a1 * qh * rf * 4, "res");
