@@ -16,7 +16,8 @@ measurement of this kernel and workload (else null).
 `secondary` holds the other configurations' lines (decode GB/s for C1 and C5; prefill TFLOP/s for C3 and
 C4 against 2.5 PFLOP/s dense fp16), each timed the same way, then the fused TurboQuant residual
 (attention_residual_tq) over a 4-bit and an 8-bit tier of C5's shape, in GB/s of codes, scales, q and residuals,
-and the cache writer (attention_cache_write_paged) placing C4's 2,048-row chunk, keys turned, in GB/s.
+the cache writer (attention_cache_write_paged) placing C4's 2,048-row chunk, keys turned, in GB/s, and GLM 5.3's
+latent attention (64 heads over 131,072 512-wide latents, row 137 with k = v) in GB/s with its TFLOP/s beside.
 
 `cpu_baseline` is the reference's own x86_avx2 silicon family (oracle/_ref, built from the reference's
 sources) over the same batch, its doors called through its nn table on the host cores — both of the
@@ -54,7 +55,7 @@ def parse():
     ap.add_argument("--cpu-threads", type=int, default=int(os.environ.get("BENCH_CPU_THREADS", "16")))
     ap.add_argument("--only", type=int, default=0,
                     help="time only this config (1-5: BASELINE.json's; 6, 7: a 4-bit / 8-bit TurboQuant tier; 8: the "
-                         "cache writer on C4's chunk), no CPU leg")
+                         "cache writer on C4's chunk; 9: GLM 5.3's latent attention), no CPU leg")
     ap.add_argument("--copy-probe", action="store_true",
                     help="run a plain 1 GiB device-to-device copy 5 times and exit: the known-size kernel the "
                          "FETCH_SIZE / WRITE_SIZE counters are scaled by")
@@ -181,6 +182,23 @@ def bench_tier(w, dev, steps, warmup):
     }, res
 
 
+def bench_latent(w, dev, steps, warmup):
+    """Latent attention (row 137, k = v): GB/s of latents read once, q and o, and the TFLOP/s of the two
+    contractions (4·heads·latent_dim a position) beside it — the shape sits near the ridge of both rooflines."""
+    step, out, over = decode_setup(w, dev)
+    wall, split_ms, others = time_steps(step, steps, warmup, "decode_split")
+    pos = int(w.lens.astype("int64").sum())
+    b = pos * w.head_dim * 2 + 2 * w.rows * w.q_heads * w.head_dim * 2
+    f = 4 * w.q_heads * w.head_dim * pos
+    merge_ms = others["decode_merge"][0] / max(others["decode_merge"][1], 1)
+    return {
+        "config": w.name, "unit": "GB/s", "value": b * steps / wall / 1e9, "ms_per_step": wall / steps * 1e3,
+        "bytes_per_step": b, "flops_per_step": f, "split_ms": split_ms, "merge_ms": merge_ms,
+        "kernel_gbs": b / (split_ms * 1e-3) / 1e9, "frac": b / (split_ms * 1e-3) / 1e9 / HBM_PEAK_GBS,
+        "kernel_tflops": f / (split_ms * 1e-3) / 1e12,
+    }, out
+
+
 def bench_write(w, dev, steps, warmup):
     """The cache writer (attention_cache_write_paged): a chunk's keys turned and its keys and values placed in
     their pages, GB/s of rows read and written and angles read."""
@@ -271,6 +289,10 @@ def main():
         print(json.dumps({"copy_probe_bytes": src.numel() * 2, "launches": 5}), flush=True)
         return
 
+    if a.only in W.LATENTS:
+        r = bench_latent(W.LATENTS[a.only](dev=dev), dev, a.steps, a.warmup)[0]
+        print(json.dumps(r), flush=True)
+        return
     if a.only in W.WRITES:
         r = bench_write(W.WRITES[a.only](dev=dev), dev, a.steps, a.warmup)[0]
         print(json.dumps(r), flush=True)
@@ -304,6 +326,10 @@ def main():
         for n in sorted(W.WRITES):
             w = W.WRITES[n](dev=dev)
             secondary.append(bench_write(w, dev, max(5, a.steps // 2), a.warmup)[0])
+            del w
+        for n in sorted(W.LATENTS):
+            w = W.LATENTS[n](dev=dev)
+            secondary.append(bench_latent(w, dev, max(5, a.steps // 2), a.warmup)[0])
             del w
         torch.cuda.empty_cache()
     cpu = None if a.no_cpu else cpu_baseline(w2, a.cpu_threads)

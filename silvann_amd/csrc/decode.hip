@@ -110,8 +110,9 @@ __device__ __forceinline__ const uint16_t* group_base(const uint16_t* plane, con
 // four groups' chunks in different banks.
 __device__ __forceinline__ int vslot(int key, int chunk) { return chunk ^ (((key >> 2) & 3) << 1); }
 
-// Keys a wave takes a step: 32 KB of K and V (16 KB each) at every head width.
-constexpr int tile_keys(int hd) { return 8192 / hd; }
+// Keys a wave takes a step: 32 KB of K and V (16 KB each) up to head_dim 256; at 512, 32 keys (64 KB), the least a
+// P·V k-step takes.
+constexpr int tile_keys(int hd) { return 8192 / hd < 32 ? 32 : 8192 / hd; }
 // Cache policy of the streamed K/V loads: non-temporal (read once, kept out of the caches' way).
 constexpr int kCacheStream = 2;
 // Which of decode_split's cache-policy variants runs (SILVANN_GFX950_DECODE_VARIANT overrides).
@@ -121,8 +122,13 @@ constexpr int kDefaultVariant = 2;
 // a tile, so each 16-key group of a tile is looked up on its own; otherwise one lookup a tile.
 // PERSISTENT: the grid is what the chip holds at once and each workgroup takes items from the counter;
 // otherwise one workgroup an item (workgroup x is item x; past the last item it returns at once).
-template <int HD, int VARIANT, bool GROUPED, bool PERSISTENT>
-__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))) void decode_split(DecodeArgs a) {
+// SHARED: the keys are the values (k == v: multi-head latent attention, where one cache of latents is both,
+// engine/src/packages/ai_z__glm_5_3/cpu/opcodes/layer__abi.cuh:283-289): each tile comes into LDS once and the
+// S^T A operand is read from there. Two waves a SIMD up to head_dim 256; one at 512 (its accumulator alone is
+// 128 registers a lane).
+template <int HD, int VARIANT, bool GROUPED, bool PERSISTENT, bool SHARED = false>
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(HD >= 512 ? 1 : 2, HD >= 512 ? 1 : 2)))
+void decode_split(DecodeArgs a) {
     constexpr int TK = tile_keys(HD);  // keys a wave takes a step: 32 KB of K and V whatever the head width
     constexpr int MT = TK / 16;      // 16-key M tiles of S^T
     constexpr int KS = HD / 32;      // k-steps of the S^T MFMA (32 dims each)
@@ -199,14 +205,18 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
         }
 
         // K as the A operand: lane (col, grp) reads key 16·p + col, dims 32·ks + 8·grp .. +8. Keys past the
-        // split read key 0 of the tile (their scores are masked). Streamed once: non-temporal.
+        // split read key 0 of the tile (their scores are masked). Streamed once: non-temporal. (SHARED: from
+        // the tile in LDS, below.)
         f16x8 kr[MT][KS];
+        if constexpr (!SHARED) {
 #pragma unroll
-        for (int p = 0; p < MT; ++p) {
-            const int key = 16 * p + col;
-            const f16x8* kk = (const f16x8*)at(kg, key < (int)nvalid ? key : 0) + grp;
+            for (int p = 0; p < MT; ++p) {
+                const int key = 16 * p + col;
+                const f16x8* kk = (const f16x8*)at(kg, key < (int)nvalid ? key : 0) + grp;
 #pragma unroll
-            for (int ks = 0; ks < KS; ++ks) kr[p][ks] = (VARIANT & 1) ? __builtin_nontemporal_load(kk + 4 * ks) : kk[4 * ks];
+                for (int ks = 0; ks < KS; ++ks)
+                    kr[p][ks] = (VARIANT & 1) ? __builtin_nontemporal_load(kk + 4 * ks) : kk[4 * ks];
+            }
         }
         // V straight into LDS: the load of step i writes slots 64·i .. 64·i + 63, one a lane; slot (key, c)
         // holds the row's chunk c ^ f(key). Keys past the split bring key 0 of the tile (weight 0).
@@ -218,6 +228,17 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
                                              16, 0, (VARIANT & 2) ? kCacheStream : 0);
         }
 
+        if constexpr (SHARED) {
+            // the tile landed; key 16·p + col's chunk 4·ks + grp sits at slot chunk ^ f(key) of its row
+            __builtin_amdgcn_s_waitcnt(0x0F70);   // vmcnt(0)
+            __builtin_amdgcn_wave_barrier();
+#pragma unroll
+            for (int p = 0; p < MT; ++p) {
+                const int key = 16 * p + col;
+#pragma unroll
+                for (int ks = 0; ks < KS; ++ks) kr[p][ks] = *(const f16x8*)(vs + (key * CPR + vslot(key, 4 * ks + grp)) * 8);
+            }
+        }
         // S^T: lane holds keys 16·p + 4·grp + r of head col.
         float sv[MT * 4];
 #pragma unroll
@@ -433,13 +454,12 @@ uint64_t resident_groups() {
 uint32_t head_blocks(uint64_t q_heads, uint64_t kv_heads) { return (uint32_t)((q_heads / kv_heads + 15) / 16); }
 
 bool decode_shape_ok(uint64_t q_heads, uint64_t kv_heads, uint64_t head_dim, uint64_t most, uint64_t rows) {
-    return (head_dim == 64 || head_dim == 128 || head_dim == 256) && kv_heads > 0 && q_heads % kv_heads == 0 &&
+    return (head_dim == 64 || head_dim == 128 || head_dim == 256 || head_dim == 512) && kv_heads > 0 && q_heads % kv_heads == 0 &&
            rows > 0 && rows <= 65535 && most > 0 && most < (1ull << 31) && kv_heads * head_blocks(q_heads, kv_heads) <= 65535;
 }
 
 }  // namespace
 
-// Launched by the door below and by the deferred scores+mix pair in doors.hip.
 void decode_paged_launch(uint16_t* o, const uint16_t* q, const uint16_t* k, const uint16_t* v, const uint32_t* pages,
                          uint64_t pages_row, uint64_t page_size, uint64_t k_row, const uint32_t* lens,
                          uint64_t q_heads, uint64_t kv_heads, uint64_t head_dim, uint64_t most, uint64_t rows,
@@ -485,7 +505,17 @@ void decode_paged_launch(uint16_t* o, const uint16_t* q, const uint16_t* k, cons
     const bool persistent = mode > 0;
     decode_plan<<<1, 256, 0, st>>>(lens, a.rows, a.chunk, (uint32_t*)a.plan, a.counter);
     prof_begin(kProfDecodeSplit);
-    switch (head_dim * 4 + variant) {
+    // head_dim 512: one workgroup an item; the shared-tile form when the keys are the values
+    const bool shared = k == v;
+    if (head_dim == 512) {
+        if (shared) {
+            if (grouped) decode_split<512, 2, true, false, true><<<igrid, kThreads, 0, st>>>(a);
+            else decode_split<512, 2, false, false, true><<<igrid, kThreads, 0, st>>>(a);
+        } else {
+            if (grouped) decode_split<512, 2, true, false><<<igrid, kThreads, 0, st>>>(a);
+            else decode_split<512, 2, false, false><<<igrid, kThreads, 0, st>>>(a);
+        }
+    } else switch (head_dim * 4 + variant) {
 #define SILVANN_DECODE_CASE(HDV, VAR) \
         case HDV * 4 + VAR: \
             if (persistent) { \
@@ -511,7 +541,8 @@ void decode_paged_launch(uint16_t* o, const uint16_t* q, const uint16_t* k, cons
     switch (head_dim) {
         case 64: SILVANN_MERGE(64) break;
         case 128: SILVANN_MERGE(128) break;
-        default: SILVANN_MERGE(256) break;
+        case 256: SILVANN_MERGE(256) break;
+        default: SILVANN_MERGE(512) break;
     }
 #undef SILVANN_MERGE
     prof_end(kProfDecodeMerge);

@@ -427,3 +427,31 @@ def cache_write_paged(k_cache, v_cache, pages, positions, k, v, cs, kv_heads, he
     doors.attention_cache_write_paged(k_cache, v_cache, pages, pages_row, page_size, capacity, positions, rows_per_seq,
                                       k, v, cs, rot if cs is not None else 0, rows, kv_heads, head_dim, over)
     return over
+
+
+# ── multi-head latent attention (GLM 5.3, DeepSeek) ──────────────────────────────────────────────────────────
+
+def latent_attention(q, latents, lens, out, heads, latent_dim, most, k_row=0, scratch=None, over=None):
+    """The latent attention of GLM 5.3's MLA (ai_z__glm_5_3/cpu/opcodes/layer__abi.cuh:283-289 for one query,
+    1037-1043 for a block of rows over their gathered sets): `heads` query heads over one cache of latents that are
+    both the keys and the values — scores_grouped(_rows) + softmax_rows / softmax_lens + mix(_rows) with one kv head
+    — in one pass of the split-K decode door (row 137) with k = v, each latent read once. Row u's `heads` queries at
+    q + u·heads·latent_dim attend latents 0 .. lens[u]-1 at latents + u·k_row; its answers go to
+    out + u·heads·latent_dim. `lens` a uint32 GPU tensor, `most` ≥ every one."""
+    heads, latent_dim, most = _dim(heads), _dim(latent_dim), _dim(most)
+    rows = lens.numel()
+    if rows == 0 or latent_dim not in (64, 128, 256, 512):
+        raise Fault(FAULT_TYPE)
+    if (not _fits(rows * heads * latent_dim, room(q)) or not _fits(rows * heads * latent_dim, room(out))
+            or not _fits((rows - 1) * k_row + most * latent_dim, room(latents))):
+        raise Fault(FAULT_BOUNDS)
+    need = decode_paged_scratch_bytes(heads, 1, latent_dim, most, rows)
+    if scratch is None:
+        scratch = torch.empty(max(need, 4), dtype=torch.uint8, device=q.device)
+    elif scratch.numel() * scratch.element_size() < need:
+        raise Fault(FAULT_BOUNDS)
+    if over is None:
+        over = torch.zeros(1, dtype=torch.int32, device=q.device)
+    doors.attention_decode_paged(out, q, latents, latents, None, 0, 0, k_row, lens, heads, 1, latent_dim, most, rows,
+                                 scratch, over)
+    return out

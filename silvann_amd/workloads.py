@@ -308,3 +308,19 @@ def write_c4(seed=8, dev=None) -> Write:
 
 
 WRITES = {8: write_c4}
+
+
+def latent(name, heads, latent_dim, lens, seed=0, dev=None) -> Decode:
+    """Latent attention as row 137 takes it: `heads` query heads, one kv head, contiguous per-row caches of latents
+    (v is the same tensor as k: the latents are both)."""
+    w = decode(name, heads, 1, latent_dim, lens, page_size=0, seed=seed, dev=dev)
+    w.v = w.k
+    return w
+
+
+def latent_glm(seed=9, dev=None) -> Decode:
+    """GLM 5.3's latent attention over a dense cache: one decode query, 64 heads, 512-wide latents, 131,072 of them."""
+    return latent("latent_64h_lat512_len131072", 64, 512, [131072], seed=seed, dev=dev)
+
+
+LATENTS = {9: latent_glm}

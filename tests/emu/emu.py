@@ -95,12 +95,13 @@ def run_causal_res(w, env: dict | None = None, timeout: int = 900):
     return _run({"q": w.q, "k": w.k, "v": w.v, "pages": pages}, params, env, timeout, outs=(("res", np.float32),))
 
 
-def run_decode(w, env: dict | None = None, timeout: int = 900):
+def run_decode(w, env: dict | None = None, timeout: int = 900, shared: bool = False):
+    """`shared`: the keys are the values — one buffer passed as both (w.v is not used)."""
     pages = None if w.pages is None else w.pages.astype(np.uint32)
     params = (f"decode {w.q_heads} {w.kv_heads} {w.head_dim} {w.most} {w.rows} {w.page_size} {w.pages_row} "
               f"{w.k_row}")
-    return _run({"q": w.q, "k": w.k, "v": w.v, "pages": pages, "lens": w.lens.astype(np.uint32)}, params, env,
-                timeout)
+    return _run({"q": w.q, "k": w.k, "v": None if shared else w.v, "pages": pages, "lens": w.lens.astype(np.uint32)},
+                params, env, timeout)
 
 
 def run_tq(q, codes, scales, qh, kvh, hd, length, d, rows=0, timeout: int = 900):

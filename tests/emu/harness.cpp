@@ -94,6 +94,7 @@ int main(int argc, char** argv) {
     char* q = load(d + "/q.bin", "q");
     char* k = load(d + "/k.bin", "k");
     char* v = load(d + "/v.bin", "v");
+    if (!v) v = k;   // no values of their own: the keys are the values (latent attention)
     char* pages = load(d + "/pages.bin", "pages");
     unsigned int* over = (unsigned int*)guarded(4, "over");
     *over = 0;

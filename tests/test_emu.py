@@ -76,3 +76,18 @@ def test_causal_residual_kernel(oracle, hd, qh, kvh, first, rows, ps):
     want = oracle.residual_mix_rows(res, p, v, qh, kvh, hd, first, rows)
     residual_parity(got, want, hd)
     assert over == 0
+
+
+@pytest.mark.parametrize("qh,lens,ps,shared", [
+    (64, [300, 41], 0, True),       # latent attention's shape: 64 heads, one kv head, keys = values, 512 wide
+    (20, [97], 64, True),           # two head blocks, the second part-full; paged
+    (16, [130, 1], 0, False),       # head_dim 512 with values of their own
+])
+def test_decode_head_dim_512(oracle, qh, lens, ps, shared):
+    """Row 137 at head_dim 512 (the shared-tile form when k == v) against the oracle's decode over the same cache."""
+    w = W.decode("emu", qh, 1, 512, lens, page_size=ps, seed=qh + len(lens))
+    got, over, _ = emu.run_decode(w, shared=shared)
+    v = w.k if shared else w.v
+    want, _ = oracle.decode_paged(w.q, w.k, v, w.pages, w.pages_row, w.page_size, w.k_row, w.lens, qh, 1, 512, w.rows)
+    parity(got, want)
+    assert over == 0
