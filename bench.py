@@ -19,6 +19,9 @@ C4 against 2.5 PFLOP/s dense fp16), each timed the same way, then the fused Turb
 the cache writer (attention_cache_write_paged) placing C4's 2,048-row chunk, keys turned, in GB/s, and GLM 5.3's
 latent attention (64 heads over 131,072 512-wide latents, row 137 with k = v) in GB/s with its TFLOP/s beside.
 
+The TurboQuant, writer and latent lines run as child processes (`--only 6`..`9`), each under a time limit, so a
+failure there is recorded in its entry and cannot take the headline down.
+
 `cpu_baseline` is the reference's own x86_avx2 silicon family (oracle/_ref, built from the reference's
 sources) over the same batch, its doors called through its nn table on the host cores — both of the
 reference's decode routes (attention_scores + attention_mix; attention_weights + attention_residual_mix +
@@ -221,6 +224,22 @@ def bench_write(w, dev, steps, warmup):
     }, None
 
 
+def isolated(n, steps, warmup, limit=240):
+    """`bench.py --only n` in a child process: the lines of kernels not yet measured on this hardware cannot take
+    the headline down with them. Its JSON line, or what went wrong."""
+    import subprocess
+    cmd = [sys.executable, str(Path(__file__).resolve()), "--only", str(n), "--steps", str(steps), "--warmup",
+           str(warmup)]
+    try:
+        r = subprocess.run(cmd, capture_output=True, text=True, timeout=limit)
+    except subprocess.TimeoutExpired:
+        return {"only": n, "error": f"no answer within {limit} s"}
+    lines = [ln for ln in r.stdout.splitlines() if ln.startswith("{")]
+    if r.returncode != 0 or not lines:
+        return {"only": n, "error": f"exit {r.returncode}: {r.stderr.strip()[-300:]}"}
+    return json.loads(lines[-1])
+
+
 def cpu_baseline(w, threads):
     """The reference x86_avx2 family over the whole C2 batch (both decode routes, the faster reported); the C
     restatement on one core as "port" where oracle/_ref is absent."""
@@ -319,19 +338,9 @@ def main():
             w = W.CONFIGS[n](dev=dev)
             secondary.append(bench_causal(w, dev, max(3, a.steps // 4), min(a.warmup, 2))[0])
             del w
-        for n in sorted(W.TIERS):
-            w = W.TIERS[n](dev=dev)
-            secondary.append(bench_tier(w, dev, max(5, a.steps // 2), a.warmup)[0])
-            del w
-        for n in sorted(W.WRITES):
-            w = W.WRITES[n](dev=dev)
-            secondary.append(bench_write(w, dev, max(5, a.steps // 2), a.warmup)[0])
-            del w
-        for n in sorted(W.LATENTS):
-            w = W.LATENTS[n](dev=dev)
-            secondary.append(bench_latent(w, dev, max(5, a.steps // 2), a.warmup)[0])
-            del w
         torch.cuda.empty_cache()
+        for n in sorted([*W.TIERS, *W.WRITES, *W.LATENTS]):
+            secondary.append(isolated(n, max(5, a.steps // 2), a.warmup))
     cpu = None if a.no_cpu else cpu_baseline(w2, a.cpu_threads)
 
     line = {

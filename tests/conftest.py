@@ -14,6 +14,18 @@ def pytest_configure(config):
     config.addinivalue_line("markers", "gpu: needs an MI355X (runs the HIP library)")
 
 
+# GPU suites whose kernels have passed on an MI355X run first, so that under `pytest -x` a failure in a newer suite
+# cannot hide their results; the rest keep their collection order after them.
+GPU_FIRST = ("test_gpu_decode.py", "test_gpu_doors.py", "test_gpu_prefill.py")
+
+
+def pytest_collection_modifyitems(config, items):
+    def rank(item):
+        name = Path(str(item.fspath)).name
+        return GPU_FIRST.index(name) if name in GPU_FIRST else len(GPU_FIRST)
+    items[:] = sorted(items, key=rank)
+
+
 @pytest.fixture(scope="session")
 def oracle():
     from oracle.oracle import ORACLE_SO, Oracle
