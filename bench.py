@@ -20,7 +20,8 @@ the cache writer (attention_cache_write_paged) placing C4's 2,048-row chunk, key
 latent attention (64 heads over 131,072 512-wide latents, row 137 with k = v) in GB/s with its TFLOP/s beside.
 
 The TurboQuant, writer and latent lines run as child processes (`--only 6`..`9`), each under a time limit, so a
-failure there is recorded in its entry and cannot take the headline down.
+failure there is recorded in its entry and cannot take the headline down; so does C2 once more with the split-K
+decode's fused finish (SILVANN_GFX950_DECODE_FUSED=1), the candidate for its default.
 
 `cpu_baseline` is the reference's own x86_avx2 silicon family (oracle/_ref, built from the reference's
 sources) over the same batch, its doors called through its nn table on the host cores — both of the
@@ -224,20 +225,23 @@ def bench_write(w, dev, steps, warmup):
     }, None
 
 
-def isolated(n, steps, warmup, limit=240):
-    """`bench.py --only n` in a child process: the lines of kernels not yet measured on this hardware cannot take
-    the headline down with them. Its JSON line, or what went wrong."""
+def isolated(n, steps, warmup, limit=240, env=None, variant=None):
+    """`bench.py --only n` in a child process (with `env` added): the lines of kernels not yet measured on this
+    hardware cannot take the headline down with them. Its JSON line, or what went wrong; `variant` names it."""
     import subprocess
     cmd = [sys.executable, str(Path(__file__).resolve()), "--only", str(n), "--steps", str(steps), "--warmup",
            str(warmup)]
     try:
-        r = subprocess.run(cmd, capture_output=True, text=True, timeout=limit)
+        r = subprocess.run(cmd, capture_output=True, text=True, timeout=limit, env={**os.environ, **(env or {})})
     except subprocess.TimeoutExpired:
-        return {"only": n, "error": f"no answer within {limit} s"}
+        return {"only": n, "variant": variant, "error": f"no answer within {limit} s"}
     lines = [ln for ln in r.stdout.splitlines() if ln.startswith("{")]
     if r.returncode != 0 or not lines:
-        return {"only": n, "error": f"exit {r.returncode}: {r.stderr.strip()[-300:]}"}
-    return json.loads(lines[-1])
+        return {"only": n, "variant": variant, "error": f"exit {r.returncode}: {r.stderr.strip()[-300:]}"}
+    out = json.loads(lines[-1])
+    if variant:
+        out["variant"] = variant
+    return out
 
 
 def cpu_baseline(w, threads):
@@ -341,6 +345,8 @@ def main():
         torch.cuda.empty_cache()
         for n in sorted([*W.TIERS, *W.WRITES, *W.LATENTS]):
             secondary.append(isolated(n, max(5, a.steps // 2), a.warmup))
+        secondary.append(isolated(2, a.steps, a.warmup, env={"SILVANN_GFX950_DECODE_FUSED": "1"},
+                                  variant="fused finish (no merge launch)"))
     cpu = None if a.no_cpu else cpu_baseline(w2, a.cpu_threads)
 
     line = {

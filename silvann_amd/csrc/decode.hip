@@ -57,15 +57,31 @@ struct DecodeArgs {
     const uint32_t* plan;   // plan[u]: splits of rows before u; plan[rows]: all splits
     uint32_t* counter;      // the next work item
     uint32_t rows;
+    // the fused finish: a count of finished splits a (row, kv head, head block), the answers, the fault word
+    uint32_t* done;
+    uint16_t* o;
+    unsigned int* over;
 };
 
-// The scratch: the work counter, the plan, then the partial residuals [row][q head][split][head_dim + 2].
+// The scratch: the work counter, the plan, the finished-split counts (rows · kv heads · head blocks), then the
+// partial residuals [row][q head][split][head_dim + 2].
 constexpr uint64_t kPlanAt = 64;
-uint64_t part_at(uint64_t rows) { return (kPlanAt + 4 * (rows + 1) + 255) / 256 * 256; }
+uint64_t done_at(uint64_t rows) { return kPlanAt + 4 * (rows + 1); }
+uint64_t part_at(uint64_t rows, uint64_t units) { return (done_at(rows) + 4 * rows * units + 255) / 256 * 256; }
 
-// Each row's split count, prefix-summed into plan[0..rows], and the counter zeroed. One workgroup.
+// Each row's split count, prefix-summed into plan[0..rows], and the counter zeroed. One workgroup. FUSED: also
+// the finished-split counts zeroed, and the answers of rows with no positions written as zeros (no split of
+// theirs will finish them).
+template <bool FUSED = false>
 __global__ __launch_bounds__(256) void decode_plan(const uint32_t* lens, uint32_t rows, uint32_t chunk, uint32_t* plan,
-                                                   uint32_t* counter) {
+                                                   uint32_t* counter, uint32_t* done = nullptr, uint32_t units = 0,
+                                                   uint16_t* o = nullptr, uint32_t row_halves = 0) {
+    if constexpr (FUSED) {
+        for (uint32_t i = threadIdx.x; i < rows * units; i += 256) done[i] = 0;
+        for (uint32_t u = 0; u < rows; ++u)
+            if (lens[u] == 0)
+                for (uint32_t i = threadIdx.x; i < row_halves; i += 256) o[(uint64_t)u * row_halves + i] = 0;
+    }
     __shared__ uint32_t scan[256];
     __shared__ uint32_t carry;
     if (threadIdx.x == 0) {
@@ -126,7 +142,9 @@ constexpr int kDefaultVariant = 2;
 // engine/src/packages/ai_z__glm_5_3/cpu/opcodes/layer__abi.cuh:283-289): each tile comes into LDS once and the
 // S^T A operand is read from there. Two waves a SIMD up to head_dim 256; one at 512 (its accumulator alone is
 // 128 registers a lane).
-template <int HD, int VARIANT, bool GROUPED, bool PERSISTENT, bool SHARED = false>
+// FUSED: the split that finishes last for its (row, kv head, head block) — it counts the finished splits — merges
+// them and writes the answers, as decode_merge does; no second launch.
+template <int HD, int VARIANT, bool GROUPED, bool PERSISTENT, bool SHARED = false, bool FUSED = false>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(HD >= 512 ? 1 : 2, HD >= 512 ? 1 : 2)))
 void decode_split(DecodeArgs a) {
     constexpr int TK = tile_keys(HD);  // keys a wave takes a step: 32 KB of K and V whatever the head width
@@ -146,6 +164,7 @@ void decode_split(DecodeArgs a) {
     const uint32_t GH = a.kv_heads * a.hblocks;
     const uint32_t total = a.plan[a.rows] * GH;
     __shared__ uint32_t item_at;
+    __shared__ uint32_t is_last;
     // the first item is the workgroup's own index; each next one comes from the counter (which counts past
     // the grid), asked for at the start of an item and read at its end so the atomic's trip is hidden
     uint32_t item = blockIdx.x;
@@ -329,6 +348,44 @@ void decode_split(DecodeArgs a) {
             pr[1] = lsum;
         }
     }
+    if constexpr (FUSED) {
+        // Release this split's residual device-wide, then count it in; the split that makes the count whole
+        // acquires the others' and finishes the heads.
+        __threadfence();
+        __syncthreads();
+        const uint32_t ns = (len + a.chunk - 1) / a.chunk;
+        if (threadIdx.x == 0) is_last = atomicAdd(a.done + (uint64_t)u * GH + gh, 1u) == ns - 1;
+        __syncthreads();
+        if (is_last) {
+            __threadfence();
+            const float* base = a.part + ((uint64_t)u * a.q_heads + h0) * a.nsplit * (HD + 2);
+            // a wave a head at a time: the largest m over the splits, then l = Σ e^(m_s - M)·l_s
+            for (int hh = w; hh < nh; hh += kWaves) {
+                const float* ph = base + (uint64_t)hh * a.nsplit * (HD + 2);
+                float mm = -INFINITY;
+                for (uint32_t q = lane; q < ns; q += 64) mm = fmaxf(mm, ph[(uint64_t)q * (HD + 2)]);
+                mm = wave_max(mm);
+                float ll = 0.0f;
+                for (uint32_t q = lane; q < ns; q += 64) ll += fast_exp(ph[(uint64_t)q * (HD + 2)] - mm) * ph[(uint64_t)q * (HD + 2) + 1];
+                ll = wave_sum(ll);
+                if (lane == 0) {
+                    ms[hh] = mm;
+                    ls[hh] = ll;
+                }
+            }
+            __syncthreads();
+            bool hit = false;
+            for (int idx = threadIdx.x; idx < nh * HD; idx += kThreads) {
+                const int hh = idx / HD, d = idx % HD;
+                const float* ph = base + (uint64_t)hh * a.nsplit * (HD + 2);
+                const float mm = ms[hh];
+                float acc = 0.0f;
+                for (uint32_t q = 0; q < ns; ++q) acc += fast_exp(ph[(uint64_t)q * (HD + 2)] - mm) * ph[(uint64_t)q * (HD + 2) + 2 + d];
+                a.o[((uint64_t)u * a.q_heads + h0 + hh) * HD + d] = to_half(acc / ls[hh], hit);
+            }
+            if (hit) *a.over = kFaultOverflow;
+        }
+    }
     if (!PERSISTENT) break;
     if (threadIdx.x == 0) item_at = next;
     __syncthreads();   // the merge area is read before the next item's tiles land in it; item_at is written
@@ -482,8 +539,11 @@ void decode_paged_launch(uint16_t* o, const uint16_t* q, const uint16_t* k, cons
     a.scale = 1.0f / sqrtf((float)head_dim);
     a.counter = (uint32_t*)scratch;
     a.plan = (const uint32_t*)((char*)scratch + kPlanAt);
-    a.part = (float*)((char*)scratch + part_at(rows));
+    a.done = (uint32_t*)((char*)scratch + done_at(rows));
+    a.part = (float*)((char*)scratch + part_at(rows, kv_heads * a.hblocks));
     a.rows = (uint32_t)rows;
+    a.o = o;
+    a.over = over;
     const dim3 mgrid((uint32_t)q_heads, (uint32_t)rows, (uint32_t)(head_dim / 64));
     hipStream_t st = stream();
     static const int variant = [] {
@@ -503,6 +563,30 @@ void decode_paged_launch(uint16_t* o, const uint16_t* q, const uint16_t* k, cons
     // measured: one workgroup an item beats the queue at both benchmark shapes (C2 5.17 vs 4.87 TB/s,
     // C5 6.2 vs 5.1), so the queue is opt-in
     const bool persistent = mode > 0;
+    // the fused finish (SILVANN_GFX950_DECODE_FUSED=1): checked in the CPU emulation, not yet measured on a GPU
+    static const bool fused = [] {
+        const char* e = getenv("SILVANN_GFX950_DECODE_FUSED");
+        return e && strtol(e, nullptr, 10) > 0;
+    }();
+    if (fused && head_dim <= 256 && !persistent) {
+        const uint32_t units = a.kv_heads * a.hblocks;
+        decode_plan<true><<<1, 256, 0, st>>>(lens, a.rows, a.chunk, (uint32_t*)a.plan, a.counter, a.done, units, o,
+                                             a.q_heads * (uint32_t)head_dim);
+        prof_begin(kProfDecodeSplit);
+        const uint32_t hv = (uint32_t)head_dim;
+        if (grouped) {
+            if (hv == 64) decode_split<64, kDefaultVariant, true, false, false, true><<<igrid, kThreads, 0, st>>>(a);
+            else if (hv == 128) decode_split<128, kDefaultVariant, true, false, false, true><<<igrid, kThreads, 0, st>>>(a);
+            else decode_split<256, kDefaultVariant, true, false, false, true><<<igrid, kThreads, 0, st>>>(a);
+        } else {
+            if (hv == 64) decode_split<64, kDefaultVariant, false, false, false, true><<<igrid, kThreads, 0, st>>>(a);
+            else if (hv == 128) decode_split<128, kDefaultVariant, false, false, false, true><<<igrid, kThreads, 0, st>>>(a);
+            else decode_split<256, kDefaultVariant, false, false, false, true><<<igrid, kThreads, 0, st>>>(a);
+        }
+        prof_end(kProfDecodeSplit);
+        check_launch("attention_decode_paged");
+        return;
+    }
     decode_plan<<<1, 256, 0, st>>>(lens, a.rows, a.chunk, (uint32_t*)a.plan, a.counter);
     prof_begin(kProfDecodeSplit);
     // head_dim 512: one workgroup an item; the shared-tile form when the keys are the values
@@ -553,7 +637,7 @@ uint64_t decode_paged_scratch(uint64_t q_heads, uint64_t kv_heads, uint64_t head
     if (!decode_shape_ok(q_heads, kv_heads, head_dim, most, rows)) return 0;
     const uint32_t chunk = choose_chunk(head_dim, kv_heads, head_blocks(q_heads, kv_heads), most, rows);
     const uint64_t nsplit = (most + chunk - 1) / chunk;
-    return part_at(rows) + rows * q_heads * nsplit * (head_dim + 2) * sizeof(float);
+    return part_at(rows, kv_heads * head_blocks(q_heads, kv_heads)) + rows * q_heads * nsplit * (head_dim + 2) * sizeof(float);
 }
 
 }  // namespace silvann

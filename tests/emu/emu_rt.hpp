@@ -150,6 +150,7 @@ inline void __builtin_amdgcn_global_load_lds(const void* src, void* lds, int siz
     emu::dma_issue((const char*)src, dst);
 }
 inline uint32_t atomicAdd(uint32_t* p, uint32_t v) { return __atomic_fetch_add(p, v, __ATOMIC_SEQ_CST); }
+inline void __threadfence() { __atomic_thread_fence(__ATOMIC_SEQ_CST); }
 inline unsigned int atomicCAS(unsigned int* p, unsigned int cmp, unsigned int val) {
     __atomic_compare_exchange_n(p, &cmp, val, false, __ATOMIC_SEQ_CST, __ATOMIC_SEQ_CST);
     return cmp;

@@ -103,7 +103,7 @@ int main(int argc, char** argv) {
     if (std::string(mode) == "causal") {   // a0 = first, a1 = rows
         on = a1 * qh * hd * 2;
         o = guarded(on, "o");
-        memset(o, 0, on);
+        memset(o, 0xFF, on);   // NaN halves: every answer must be written
         silvann_gfx950_attention_causal_paged((uint16_t*)o, (const uint16_t*)q, (const uint16_t*)k, (const uint16_t*)v,
                                               (const uint32_t*)pages, ps, qh, kvh, hd, a0, a1, over);
     } else if (std::string(mode) == "cache") {
@@ -175,7 +175,7 @@ int main(int argc, char** argv) {
         char* lens = load(d + "/lens.bin", "lens");
         on = a1 * qh * hd * 2;
         o = guarded(on, "o");
-        memset(o, 0, on);
+        memset(o, 0xFF, on);   // NaN halves: every answer must be written
         const uint64_t sb = silvann_gfx950_attention_decode_paged_scratch(qh, kvh, hd, a0, a1);
         float* scratch = (float*)guarded(sb ? sb : 4, "scratch");
         memset(scratch, 0xFF, sb ? sb : 4);   // whatever a caller's scratch held before

@@ -91,3 +91,22 @@ def test_decode_head_dim_512(oracle, qh, lens, ps, shared):
     want, _ = oracle.decode_paged(w.q, w.k, v, w.pages, w.pages_row, w.page_size, w.k_row, w.lens, qh, 1, 512, w.rows)
     parity(got, want)
     assert over == 0
+
+
+FUSED = {"SILVANN_GFX950_DECODE_FUSED": "1"}
+
+
+@pytest.mark.parametrize("qh,kvh,hd,lens,ps", [
+    (16, 2, 256, [700, 2048, 0], 256),     # a row with no positions: its answers are zeros
+    (8, 2, 128, [1, 17, 3000], 0),         # a row of many splits beside one-split rows
+    (4, 4, 64, [33, 250], 16),             # pages shorter than a tile
+])
+def test_decode_fused_finish(oracle, qh, kvh, hd, lens, ps):
+    """Row 137 with the fused finish (the last split of a row and head block merges the others): the same
+    answers as the oracle's decode, every split counted once — the scratch starts as garbage."""
+    w = W.decode("emu", qh, kvh, hd, lens, page_size=ps, seed=hd + len(lens) + 3)
+    got, over, _ = emu.run_decode(w, env=FUSED)
+    want, _ = oracle.decode_paged(w.q, w.k, w.v, w.pages, w.pages_row, w.page_size, w.k_row, w.lens, qh, kvh, hd,
+                                  w.rows)
+    parity(got, want)
+    assert over == 0
