@@ -126,3 +126,24 @@ def run_cache_write(kc, vc, pages, pages_row, page_size, capacity, positions, ro
     params = f"cache {rot} {kvh} {hd} {rows_per_seq} {rows} {page_size} {pages_row} {capacity}"
     return _run({"q": cs, "k": k, "v": v, "pages": pages, "lens": np.ascontiguousarray(positions, np.uint32),
                  "kc": kc, "vc": vc}, params, None, timeout, outs=(("kc_out", np.uint16), ("vc_out", np.uint16)))
+
+
+def run_fp16(q, k, v, qh, kvh, hd, length=0, first=0, rows=0, timeout: int = 900):
+    """attention_weights + attention_residual_mix over `length` keys (rows == 0), or their _rows forms for `rows`
+    rows from `first`: the weights, the residual after the first door and after the second."""
+    many = rows > 0
+    params = f"{'fp16_rows' if many else 'fp16'} {qh} {kvh} {hd} {first if many else length} {rows or 1} 0 0 0"
+    return _run({"q": q, "k": k, "v": v}, params, None, timeout,
+                outs=(("p", np.float32), ("res_w", np.float32), ("res", np.float32)))
+
+
+def run_grouped(q, k, v, qh, kvh, hd, most, lens=None, k_row=0, timeout: int = 900):
+    """attention_scores_grouped + attention_softmax_rows + attention_mix over `most` keys (lens None), or
+    scores_grouped_rows + softmax_lens + mix_rows for one row a lens entry: raw scores, weights and answers."""
+    many = lens is not None
+    rows = len(lens) if many else 1
+    params = f"{'grouped_rows' if many else 'grouped'} {qh} {kvh} {hd} {most} {rows} 0 0 {k_row}"
+    files = {"q": q, "k": k, "v": v}
+    if many:
+        files["lens"] = np.ascontiguousarray(lens, np.uint32)
+    return _run(files, params, None, timeout, outs=(("p", np.float32), ("p_soft", np.float32), ("o", np.uint16)))

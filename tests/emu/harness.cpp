@@ -1,5 +1,5 @@
 // harness.cpp — TEST INFRASTRUCTURE: runs one call of one of the library's entry points (causal prefill, its
-// residual form, paged decode, the TurboQuant rows, the cache writer) in the CPU emulation, on inputs and parameters a test
+// residual form, paged decode, the reference's generic rows, the TurboQuant rows, the cache writer) in the CPU emulation, on inputs and parameters a test
 // wrote to a directory, and writes the answer back there. Every buffer sits against an inaccessible page, so an out-of-bounds read or write stops the
 // run with the buffer, the offset and the lane that made it; a run that outlives its time limit (a lost
 // barrier) stops too.
@@ -106,6 +106,55 @@ int main(int argc, char** argv) {
         memset(o, 0xFF, on);   // NaN halves: every answer must be written
         silvann_gfx950_attention_causal_paged((uint16_t*)o, (const uint16_t*)q, (const uint16_t*)k, (const uint16_t*)v,
                                               (const uint32_t*)pages, ps, qh, kvh, hd, a0, a1, over);
+    } else if (std::string(mode) == "fp16" || std::string(mode) == "fp16_rows") {
+        // fp16: weights then residual_mix over a0 = length keys (one row). fp16_rows: weights_rows then
+        // residual_mix_rows, rows a1 from a0 = first. p, the residual after the first door, and after the second.
+        const bool many = std::string(mode) == "fp16_rows";
+        const unsigned long rows = many ? a1 : 1, rf = hd + 2, span = many ? a0 + a1 : a0;
+        float* p = (float*)guarded(rows * qh * span * 4, "p");
+        memset(p, 0xFF, rows * qh * span * 4);
+        float* res = (float*)guarded(rows * qh * rf * 4, "res");
+        memset(res, 0xFF, rows * qh * rf * 4);
+        if (many) silvann_gfx950_attention_weights_rows(p, res, (const uint16_t*)q, (const uint16_t*)k, qh, kvh, hd, a0, a1);
+        else silvann_gfx950_attention_weights(p, res, (const uint16_t*)q, (const uint16_t*)k, qh, kvh, hd, a0);
+        save(d + "/p.bin", p, rows * qh * span * 4);
+        save(d + "/res_w.bin", res, rows * qh * rf * 4);
+        if (many) silvann_gfx950_attention_residual_mix_rows(res, p, (const uint16_t*)v, qh, kvh, hd, a0, a1);
+        else silvann_gfx950_attention_residual_mix(res, p, (const uint16_t*)v, qh, kvh, hd, a0);
+        save(d + "/res.bin", res, rows * qh * rf * 4);
+        save(d + "/over.bin", over, 4);
+        fprintf(stderr, "emu done: refused %d, wave exchanges %ld\n", silvann::emu_refused, (long)emu::ops);
+        return silvann::emu_refused ? 5 : 0;
+    } else if (std::string(mode) == "grouped" || std::string(mode) == "grouped_rows") {
+        // grouped: scores_grouped, softmax_rows, mix over a0 = length keys. grouped_rows: scores_grouped_rows,
+        // softmax_lens, mix_rows, a1 rows over their own lens (file lens) at k + u·k_row, p rows q_heads·a0 apart.
+        const bool many = std::string(mode) == "grouped_rows";
+        const unsigned long rows = many ? a1 : 1, most = a0;
+        const unsigned long p_row = qh * most, o_row = qh * hd;
+        float* p = (float*)guarded(rows * p_row * 4, "p");
+        memset(p, 0xFF, rows * p_row * 4);
+        uint16_t* o16 = (uint16_t*)guarded(rows * o_row * 2, "o");
+        memset(o16, 0xFF, rows * o_row * 2);
+        if (many) {
+            char* lens = load(d + "/lens.bin", "lens");
+            silvann_gfx950_attention_scores_grouped_rows(p, p_row, (const uint16_t*)q, o_row, (const uint16_t*)k, k_row,
+                                                         (const uint32_t*)lens, qh, kvh, hd, most, rows);
+            save(d + "/p.bin", p, rows * p_row * 4);
+            silvann_gfx950_attention_softmax_lens(p, p_row, (const uint32_t*)lens, qh, rows);
+            save(d + "/p_soft.bin", p, rows * p_row * 4);
+            silvann_gfx950_attention_mix_rows(o16, o_row, p, p_row, (const uint16_t*)v, k_row, (const uint32_t*)lens, qh,
+                                              kvh, hd, rows, over);
+        } else {
+            silvann_gfx950_attention_scores_grouped(p, (const uint16_t*)q, (const uint16_t*)k, qh, kvh, hd, most);
+            save(d + "/p.bin", p, rows * p_row * 4);
+            silvann_gfx950_attention_softmax_rows(p, qh, most);
+            save(d + "/p_soft.bin", p, rows * p_row * 4);
+            silvann_gfx950_attention_mix(o16, p, (const uint16_t*)v, qh, kvh, hd, most, over);
+        }
+        save(d + "/o.bin", o16, rows * o_row * 2);
+        save(d + "/over.bin", over, 4);
+        fprintf(stderr, "emu done: refused %d, wave exchanges %ld\n", silvann::emu_refused, (long)emu::ops);
+        return silvann::emu_refused ? 5 : 0;
     } else if (std::string(mode) == "cache") {
         // qh = rot, a0 = rows_per_seq, a1 = rows, k_row = capacity; q holds the angles (fp32), lens the positions,
         // kc / vc the caches as they were
