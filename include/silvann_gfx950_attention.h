@@ -130,6 +130,15 @@ void silvann_gfx950_attention_mix_rows(uint16_t* o, uint64_t o_row, const float*
                                        const uint16_t* v, uint64_t v_row, const uint32_t* lens, uint64_t q_heads,
                                        uint64_t kv_heads, uint64_t head_dim, uint64_t rows, unsigned int* over);
 
+/* gpu.cuh:140 rope_rows — kernels.cuh:1710-1726: each of `rows` rows (row_stride halves apart) has its `heads` heads
+ * (head_stride apart) turned by its own angles at cs + r·rot (rot/2 cosines, then rot/2 sines): elements k and
+ * k + rot/2 of a head become a·c − b·s and b·c + a·s — as the reference's host build computes them, fma(a, c, −(b·s))
+ * and fma(b, c, a·s) — rounded to fp16, overflow storing NPOV in `over`. `o` may be `x`. The RoPE the rows verb
+ * turns its chunk's queries and keys with (attention__abi.cuh:403-406). */
+#define SILVANN_GFX950_ROW_ROPE_ROWS 46u
+void silvann_gfx950_rope_rows(uint16_t* o, const uint16_t* x, const float* cs, uint64_t rows, uint64_t heads,
+                              uint64_t head_stride, uint64_t row_stride, uint64_t rot, unsigned int* over);
+
 /* The nn door table's row count at ABI version 9 (gpu.cuh:93-230): new rows are appended after it. */
 #define SILVANN_GFX950_NN_ROWS 137u
 

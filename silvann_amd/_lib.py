@@ -38,6 +38,7 @@ SIGNATURES = {
     "silvann_gfx950_attention_scores_grouped_rows": [_p, _u64, _p, _u64, _p, _u64, _p, _u64, _u64, _u64, _u64, _u64],
     "silvann_gfx950_attention_softmax_lens": [_p, _u64, _p, _u64, _u64],
     "silvann_gfx950_attention_mix_rows": [_p, _u64, _p, _u64, _p, _u64, _p, _u64, _u64, _u64, _u64, _p],
+    "silvann_gfx950_rope_rows": [_p, _p, _p, _u64, _u64, _u64, _u64, _u64, _p],
     "silvann_gfx950_attention_decode_paged": [_p, _p, _p, _p, _p, _u64, _u64, _u64, _p, _u64, _u64, _u64, _u64, _u64,
                                               _p, _p],
     "silvann_gfx950_attention_decode_paged_scratch": [_u64, _u64, _u64, _u64, _u64],

@@ -119,6 +119,25 @@ __global__ __launch_bounds__(256) void cache_write(CacheArgs a) {
     if (out) *a.over = kFaultBounds;
 }
 
+// `rope_rows` itself (kernels.cuh:1710-1726), every row's heads turned in place or into `o`: a lane a pair, the
+// same two FMAs as the writer. Rows row_stride apart, heads head_stride apart, any alignment.
+__global__ __launch_bounds__(256) void rope_rows_kernel(uint16_t* o, const uint16_t* x, const float* cs, uint64_t rows,
+                                                        uint64_t heads, uint64_t head_stride, uint64_t row_stride,
+                                                        uint64_t rot, unsigned int* over) {
+#pragma clang fp contract(off)
+    const uint64_t pairs = rot / 2, per_row = heads * pairs, n = rows * per_row;
+    bool hit = false;
+    for (uint64_t i = (uint64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (uint64_t)gridDim.x * 256) {
+        const uint64_t r = i / per_row, rest = i - r * per_row, e = rest / pairs, k = rest - e * pairs;
+        const uint64_t at = r * row_stride + e * head_stride + k;
+        const float a = half_bits_to_float(x[at]), b = half_bits_to_float(x[at + pairs]);
+        const float c = cs[r * rot + k], s = cs[r * rot + pairs + k];
+        o[at] = to_half(__builtin_fmaf(a, c, -(b * s)), hit);
+        o[at + pairs] = to_half(__builtin_fmaf(b, c, a * s), hit);
+    }
+    if (hit) *over = kFaultOverflow;
+}
+
 }  // namespace
 }  // namespace silvann
 
@@ -158,4 +177,16 @@ SILVANN_EXPORT void silvann_gfx950_attention_cache_write_paged(uint16_t* k_cache
     else cache_write<1><<<dim3((unsigned)blocks), 256, 0, stream()>>>(a);
     prof_end(kProfCacheWrite);
     check_launch("attention_cache_write_paged");
+}
+
+SILVANN_EXPORT void silvann_gfx950_rope_rows(uint16_t* o, const uint16_t* x, const float* cs, uint64_t rows,
+                                             uint64_t heads, uint64_t head_stride, uint64_t row_stride, uint64_t rot,
+                                             unsigned int* over) {
+    using namespace silvann;
+    if (rows == 0 || heads == 0 || rot < 2) return;   // nothing to turn (the reference's loop runs no item)
+    const uint64_t n = rows * heads * (rot / 2);
+    const uint64_t blocks = std::min<uint64_t>((n + 255) / 256, 8192);
+    rope_rows_kernel<<<dim3((unsigned)blocks), 256, 0, stream()>>>(o, x, cs, rows, heads, head_stride, row_stride, rot,
+                                                                   over);
+    check_launch("rope_rows");
 }

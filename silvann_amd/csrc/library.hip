@@ -145,6 +145,7 @@ SILVANN_EXPORT uint32_t silvann_gfx950_attention_install(void* nn_doors) {
         {SILVANN_GFX950_ROW_ATTENTION_SCORES_GROUPED_ROWS, (void*)&silvann_gfx950_attention_scores_grouped_rows},
         {SILVANN_GFX950_ROW_ATTENTION_SOFTMAX_LENS, (void*)&silvann_gfx950_attention_softmax_lens},
         {SILVANN_GFX950_ROW_ATTENTION_MIX_ROWS, (void*)&silvann_gfx950_attention_mix_rows},
+        {SILVANN_GFX950_ROW_ROPE_ROWS, (void*)&silvann_gfx950_rope_rows},
         {SILVANN_GFX950_ROW_ATTENTION_DECODE_PAGED, (void*)&silvann_gfx950_attention_decode_paged},
         {SILVANN_GFX950_ROW_ATTENTION_CAUSAL_PAGED, (void*)&silvann_gfx950_attention_causal_paged},
         {SILVANN_GFX950_ROW_ATTENTION_RESIDUAL_TQ, (void*)&silvann_gfx950_attention_residual_tq},
@@ -165,5 +166,5 @@ SILVANN_EXPORT uint32_t silvann_gfx950_attention_install(void* nn_doors) {
 }
 
 SILVANN_EXPORT const char* silvann_gfx950_version(void) {
-    return "gfx950 decode-splitk-mfma16 causal-mfma32 tq-mfma16 cache-writer doors-26 v1";
+    return "gfx950 decode-splitk-mfma16 causal-mfma32 tq-mfma16 cache-writer doors-27 v1";
 }

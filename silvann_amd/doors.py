@@ -50,6 +50,7 @@ attention_residual_mix_tq_rows = _door("attention_residual_mix_tq_rows")
 attention_scores_grouped_rows = _door("attention_scores_grouped_rows")
 attention_softmax_lens = _door("attention_softmax_lens")
 attention_mix_rows = _door("attention_mix_rows")
+rope_rows = _door("rope_rows")
 attention_decode_paged = _door("attention_decode_paged")
 attention_decode_paged_scratch = _door("attention_decode_paged_scratch")
 attention_causal_paged = _door("attention_causal_paged")

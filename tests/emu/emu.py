@@ -147,3 +147,9 @@ def run_grouped(q, k, v, qh, kvh, hd, most, lens=None, k_row=0, timeout: int = 9
     if many:
         files["lens"] = np.ascontiguousarray(lens, np.uint32)
     return _run(files, params, None, timeout, outs=(("p", np.float32), ("p_soft", np.float32), ("o", np.uint16)))
+
+
+def run_rope_rows(x, cs, rows, heads, head_stride, row_stride, rot, timeout: int = 900):
+    """rope_rows in place on a copy of x (halves as uint16): the turned rows and the fault word."""
+    params = f"rope {heads} 0 {head_stride} 0 {rows} {rot} 0 {row_stride}"
+    return _run({"q": x, "k": cs}, params, None, timeout, outs=(("o", np.uint16),))

@@ -155,6 +155,16 @@ int main(int argc, char** argv) {
         save(d + "/over.bin", over, 4);
         fprintf(stderr, "emu done: refused %d, wave exchanges %ld\n", silvann::emu_refused, (long)emu::ops);
         return silvann::emu_refused ? 5 : 0;
+    } else if (std::string(mode) == "rope") {
+        // rope_rows in place: q holds x, k the angles; qh = heads, hd = head_stride, a1 = rows, ps = rot,
+        // k_row = row_stride
+        size_t xn = 0;
+        char* x = load(d + "/q.bin", "x", &xn);
+        silvann_gfx950_rope_rows((uint16_t*)x, (const uint16_t*)x, (const float*)k, a1, qh, hd, k_row, ps, over);
+        save(d + "/o.bin", x, xn);
+        save(d + "/over.bin", over, 4);
+        fprintf(stderr, "emu done: refused %d, wave exchanges %ld\n", silvann::emu_refused, (long)emu::ops);
+        return silvann::emu_refused ? 5 : 0;
     } else if (std::string(mode) == "cache") {
         // qh = rot, a0 = rows_per_seq, a1 = rows, k_row = capacity; q holds the angles (fp32), lens the positions,
         // kc / vc the caches as they were

@@ -12,8 +12,6 @@
 import numpy as np
 import pytest
 
-from oracle.oracle import FAULT_OVERFLOW
-
 FAULT_BOUNDS = 0x4E50424E
 
 
@@ -159,3 +157,19 @@ def test_emulated_writer(oracle, kvh, hd, rot, lens, rps, ps, cap, paged):
     assert go == wo
     if rot == 0:
         assert go == 0
+
+
+@pytest.mark.parametrize("rows,heads,hd,rot,row_stride", [(13, 2, 128, 128, 256), (5, 3, 72, 18, 3 * 72 + 8)])
+def test_emulated_rope_rows(oracle, rows, heads, hd, rot, row_stride):
+    """rope_rows (nn row 46) in the emulation against the oracle — itself the reference family's door to the bit."""
+    from tests.emu import emu
+    if emu.compiler() is None:
+        pytest.skip("no clang++ for the CPU emulation")
+    rng = np.random.default_rng(rows + hd)
+    x = rng.standard_normal(rows * row_stride).astype(np.float16).view(np.uint16)
+    x[5] = np.float16(65000).view(np.uint16)
+    cs = angles(rng.integers(0, 300000, rows), rot)
+    want, wo = oracle.rope_rows(x, cs, rows, heads, hd, row_stride, rot)
+    got, go, _ = emu.run_rope_rows(x, cs, rows, heads, hd, row_stride, rot)
+    assert np.array_equal(got, want)
+    assert go == wo

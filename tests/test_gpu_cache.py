@@ -80,3 +80,21 @@ def test_writer_refuses_an_odd_turn(dev):
     torch.cuda.synchronize()
     assert doors.launch_failed()
     assert int(over.item()) == 0
+
+
+def test_rope_rows_against_oracle(dev, oracle):
+    """rope_rows (nn row 46) on the GPU, bit for bit the oracle's (which is the reference family's door)."""
+    from tests.test_cache import angles
+    rows, heads, hd, rot, row_stride = 300, 16, 128, 64, 16 * 128 + 8
+    print("case: rope_rows", flush=True)
+    rng = np.random.default_rng(4)
+    x = rng.standard_normal(rows * row_stride).astype(np.float16).view(np.uint16)
+    x[11] = np.float16(65000).view(np.uint16)
+    cs = angles(rng.integers(0, 300000, rows), rot)
+    want, wo = oracle.rope_rows(x, cs, rows, heads, hd, row_stride, rot)
+    xd = t(x, dev)
+    over = torch.zeros(1, dtype=torch.int32, device=dev)
+    doors.rope_rows(xd, xd, t(cs, dev), rows, heads, hd, row_stride, rot, over)
+    assert np.array_equal(xd.cpu().numpy(), want)
+    assert (int(over.item()) & 0xFFFFFFFF) == wo
+    assert not doors.launch_failed()
