@@ -242,6 +242,19 @@ uint32_t silvann_gfx950_attention_install(void* nn_doors);
  * reference family's choice, amd_rocm_base/nn.cuh:25-34). Thread-local, as a runner thread is a worker's. */
 void silvann_gfx950_set_stream(void* stream);
 void* silvann_gfx950_get_stream(void);
+/* Deferred chains. The reference's verbs call some doors only back to back on one thread — attention_scores then
+ * attention_mix (attention__abi.cuh:155-158), attention_weights then attention_residual_mix (203-206),
+ * attention_causal_scores_grouped then attention_causal_softmax then attention_causal_mix (407-414). By default this
+ * library records such a chain's first doors instead of launching them; when the continuation arrives on the same
+ * thread and stream with the same operands, the chain runs as one fused kernel (the split-K decode of row 137, the
+ * causal prefill of row 138) and the weights buffer `p` never holds weights (the decode pairs use it as their
+ * scratch). Any other door of this library — and set_stream, launch_failed, flush — first runs what is recorded
+ * exactly as the door would have run, so any other order of calls keeps the reference's semantics. A caller that
+ * reads `p` itself after a chain's first door, or that calls a door of another library in between, calls
+ * silvann_gfx950_flush() first, or switches deferral off for its thread. SILVANN_GFX950_DEFER=0 makes off the
+ * process default. (No counterpart in the reference: the fusion its door ABI leaves no single door for.) */
+void silvann_gfx950_flush(void);
+void silvann_gfx950_set_defer(int on);
 /* Nonzero if a door on the current device refused its operands or failed to launch since the last call; clears
  * it. Kept per device, not per thread, as the reference family keeps it (the next compute_completed on that
  * device answers false, amd_rocm_base/sys.cuh:39-62 and amd_rocm_base/nn.cuh:29-33). */

@@ -50,6 +50,8 @@ SIGNATURES = {
     "silvann_gfx950_attention_residual_tq_scratch": [_u64, _u64, _u64, _u64, _u64, _u64],
     "silvann_gfx950_set_stream": [_p],
     "silvann_gfx950_get_stream": [],
+    "silvann_gfx950_flush": [],
+    "silvann_gfx950_set_defer": [C.c_int],
     "silvann_gfx950_launch_failed": [],
     "silvann_gfx950_profile_enable": [C.c_int],
     "silvann_gfx950_profile_read": [C.c_char_p, C.POINTER(C.c_double), C.POINTER(C.c_uint64)],

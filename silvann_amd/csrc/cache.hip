@@ -148,6 +148,7 @@ SILVANN_EXPORT void silvann_gfx950_attention_cache_write_paged(uint16_t* k_cache
                                                                const uint16_t* k, const uint16_t* v, const float* cs,
                                                                uint64_t rot, uint64_t rows, uint64_t kv_heads,
                                                                uint64_t head_dim, unsigned int* over) {
+    silvann::flush_deferred();
     using namespace silvann;
     const uint64_t turn = cs ? rot : 0;
     const bool ok = k_cache && v_cache && positions && k && v && over && rows > 0 && rows < (1ull << 32) &&
@@ -182,6 +183,7 @@ SILVANN_EXPORT void silvann_gfx950_attention_cache_write_paged(uint16_t* k_cache
 SILVANN_EXPORT void silvann_gfx950_rope_rows(uint16_t* o, const uint16_t* x, const float* cs, uint64_t rows,
                                              uint64_t heads, uint64_t head_stride, uint64_t row_stride, uint64_t rot,
                                              unsigned int* over) {
+    silvann::flush_deferred();
     using namespace silvann;
     if (rows == 0 || heads == 0 || rot < 2) return;   // nothing to turn (the reference's loop runs no item)
     const uint64_t n = rows * heads * (rot / 2);

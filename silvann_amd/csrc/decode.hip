@@ -468,6 +468,53 @@ __global__ __launch_bounds__(64 * kMergeWaves) void decode_merge(uint16_t* o, co
     if (hit) *over = kFaultOverflow;
 }
 
+// One row of a uniform length: its length where decode_split reads it, its one-row plan, the counter zeroed — the
+// plan of the deferred door pairs, whose one query's length is a host value.
+__global__ void decode_plan_one(uint32_t* lens, uint32_t length, uint32_t nsplit, uint32_t* plan, uint32_t* counter) {
+    if (threadIdx.x == 0) {
+        lens[0] = length;
+        plan[0] = 0;
+        plan[1] = nsplit;
+        counter[0] = 0;
+    }
+}
+
+// decode_merge's arithmetic into the reference's residual instead of an answer: res[h] = {M, Σ e^(m_s - M)·l_s,
+// Σ e^(m_s - M)·acc_s} (kernels.cuh:1243-1255 over the splits), a workgroup per (query head, 64 dims), one row.
+template <int HD>
+__global__ __launch_bounds__(256) void decode_merge_res(float* res, const float* part, uint32_t nsplit) {
+    __shared__ float red[4];
+    __shared__ float accs[4][64];
+    __shared__ float lss[4];
+    const uint32_t h = blockIdx.x;
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    const int d = blockIdx.z * 64 + lane;
+    const float* pr = part + (uint64_t)h * nsplit * (HD + 2);
+    float* out = res + (uint64_t)h * (HD + 2);
+    float mx = -INFINITY;
+    for (uint32_t s = threadIdx.x; s < nsplit; s += 256) mx = fmaxf(mx, pr[(uint64_t)s * (HD + 2)]);
+    mx = wave_max(mx);
+    if (lane == 0) red[w] = mx;
+    __syncthreads();
+    const float M = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    float acc = 0.0f, lsum = 0.0f;
+    for (uint32_t s = w; s < nsplit; s += 4) {
+        const float* x = pr + (uint64_t)s * (HD + 2);
+        const float f = fast_exp(x[0] - M);
+        acc += f * x[2 + d];
+        lsum += f * x[1];
+    }
+    accs[w][lane] = acc;
+    if (lane == 0) lss[w] = lsum;
+    __syncthreads();
+    if (w != 0) return;
+    out[2 + d] = accs[0][lane] + accs[1][lane] + accs[2][lane] + accs[3][lane];
+    if (d == 0) {
+        out[0] = M;
+        out[1] = lss[0] + lss[1] + lss[2] + lss[3];
+    }
+}
+
 // The split length: a multiple of the 4 waves' tiles, sized so the items (splits × kv heads × head blocks,
 // over the longest row for every row) about fill the chip once — more would re-pay the per-item merge,
 // fewer would leave CUs idle — and never past 1024 positions, past which the measured rate falls.
@@ -633,6 +680,77 @@ void decode_paged_launch(uint16_t* o, const uint16_t* q, const uint16_t* k, cons
     check_launch("attention_decode_paged");
 }
 
+// One query over a contiguous cache — the deferred door pairs' fused form (attention_scores + attention_mix into
+// `o`; attention_weights + attention_residual_mix into `res`). Its scratch is the pair's own weights buffer, `cap`
+// bytes, which the fused form never fills with weights: the splits are made long enough for their residuals to fit
+// it. Answers false, launching nothing, when the shape is not one decode_split takes or no split length fits.
+bool decode_one(uint16_t* o, float* res, const uint16_t* q, const uint16_t* k, const uint16_t* v, uint64_t q_heads,
+                uint64_t kv_heads, uint64_t head_dim, uint64_t length, void* scratch, uint64_t cap, unsigned int* over) {
+    if (!decode_shape_ok(q_heads, kv_heads, head_dim, length, 1) || (((uintptr_t)scratch) & 3u) != 0) return false;
+    const uint32_t hblocks = head_blocks(q_heads, kv_heads);
+    const uint64_t head = part_at(1, kv_heads * hblocks), per_split = q_heads * (head_dim + 2) * sizeof(float);
+    if (cap <= head || (cap - head) / per_split == 0) return false;
+    const uint64_t fit = (cap - head) / per_split;   // splits the scratch holds
+    const uint64_t step = (uint64_t)tile_keys((int)head_dim) * kWaves;
+    uint64_t chunk = choose_chunk(head_dim, kv_heads, hblocks, length, 1);
+    if ((length + chunk - 1) / chunk > fit) chunk = ((length + fit - 1) / fit + step - 1) / step * step;
+    const uint64_t nsplit = (length + chunk - 1) / chunk;
+    if (nsplit > fit || nsplit > kMaxSplits) return false;
+    DecodeArgs a;
+    a.q = q; a.k = k; a.v = v; a.pages = nullptr; a.pages_row = 0; a.page_size = 0; a.k_row = 0;
+    a.q_heads = (uint32_t)q_heads; a.kv_heads = (uint32_t)kv_heads; a.group = (uint32_t)(q_heads / kv_heads);
+    a.hblocks = hblocks;
+    a.chunk = (uint32_t)chunk;
+    a.nsplit = (uint32_t)nsplit;
+    a.scale = 1.0f / sqrtf((float)head_dim);
+    a.counter = (uint32_t*)scratch;
+    uint32_t* lens = (uint32_t*)((char*)scratch + 32);
+    a.lens = lens;
+    a.plan = (const uint32_t*)((char*)scratch + kPlanAt);
+    a.done = (uint32_t*)((char*)scratch + done_at(1));
+    a.part = (float*)((char*)scratch + head);
+    a.rows = 1;
+    a.o = o;
+    a.over = over;
+    hipStream_t st = stream();
+    decode_plan_one<<<1, 64, 0, st>>>(lens, (uint32_t)length, (uint32_t)nsplit, (uint32_t*)a.plan, a.counter);
+    const dim3 grid((uint32_t)(nsplit * kv_heads * hblocks));
+    prof_begin(kProfDecodeSplit);
+    if (head_dim == 512) {
+        if (k == v) decode_split<512, 2, false, false, true><<<grid, kThreads, 0, st>>>(a);
+        else decode_split<512, 2, false, false><<<grid, kThreads, 0, st>>>(a);
+    } else if (head_dim == 256) {
+        decode_split<256, kDefaultVariant, false, false><<<grid, kThreads, 0, st>>>(a);
+    } else if (head_dim == 128) {
+        decode_split<128, kDefaultVariant, false, false><<<grid, kThreads, 0, st>>>(a);
+    } else {
+        decode_split<64, kDefaultVariant, false, false><<<grid, kThreads, 0, st>>>(a);
+    }
+    prof_end(kProfDecodeSplit);
+    const dim3 mgrid((uint32_t)q_heads, 1, (uint32_t)(head_dim / 64));
+    if (o) {
+        const bool wide = nsplit > 64;
+#define SILVANN_MERGE_ONE(HDV) \
+        if (wide) decode_merge<HDV, 16><<<mgrid, 1024, 0, st>>>(o, a.part, lens, a.q_heads, a.chunk, a.nsplit, over); \
+        else decode_merge<HDV, 4><<<mgrid, 256, 0, st>>>(o, a.part, lens, a.q_heads, a.chunk, a.nsplit, over);
+        switch (head_dim) {
+            case 64: SILVANN_MERGE_ONE(64) break;
+            case 128: SILVANN_MERGE_ONE(128) break;
+            case 256: SILVANN_MERGE_ONE(256) break;
+            default: SILVANN_MERGE_ONE(512) break;
+        }
+#undef SILVANN_MERGE_ONE
+    } else {
+        switch (head_dim) {
+            case 64: decode_merge_res<64><<<mgrid, 256, 0, st>>>(res, a.part, a.nsplit); break;
+            case 128: decode_merge_res<128><<<mgrid, 256, 0, st>>>(res, a.part, a.nsplit); break;
+            case 256: decode_merge_res<256><<<mgrid, 256, 0, st>>>(res, a.part, a.nsplit); break;
+            default: decode_merge_res<512><<<mgrid, 256, 0, st>>>(res, a.part, a.nsplit); break;
+        }
+    }
+    return true;
+}
+
 uint64_t decode_paged_scratch(uint64_t q_heads, uint64_t kv_heads, uint64_t head_dim, uint64_t most, uint64_t rows) {
     if (!decode_shape_ok(q_heads, kv_heads, head_dim, most, rows)) return 0;
     const uint32_t chunk = choose_chunk(head_dim, kv_heads, head_blocks(q_heads, kv_heads), most, rows);
@@ -648,6 +766,7 @@ SILVANN_EXPORT void silvann_gfx950_attention_decode_paged(uint16_t* o, const uin
                                                           uint64_t q_heads, uint64_t kv_heads, uint64_t head_dim,
                                                           uint64_t most, uint64_t rows, float* scratch,
                                                           unsigned int* over) {
+    silvann::flush_deferred();
     silvann::decode_paged_launch(o, q, k, v, pages, pages_row, page_size, k_row, lens, q_heads, kv_heads, head_dim,
                                  most, rows, scratch, over);
 }

@@ -503,14 +503,9 @@ void launch_tq_mix(float* res, float* p, const uint8_t* codes, const uint16_t* s
         tq_mix_reduce<MODE><<<rgrid, 256, 0, st>>>(res, p, G, nsplit, split);
     }
 }
-}  // namespace
-}  // namespace silvann
-
-using namespace silvann;
-
-// gpu.cuh:119 — kernels.cuh:1133-1141
-SILVANN_EXPORT void silvann_gfx950_attention_scores(float* p, const uint16_t* q, const uint16_t* k, uint64_t q_heads,
-                                                    uint64_t kv_heads, uint64_t head_dim, uint64_t length) {
+// The chain doors' bodies: what each door launches when it runs on its own (and what a flush runs).
+void scores_body(float* p, const uint16_t* q, const uint16_t* k, uint64_t q_heads, uint64_t kv_heads,
+                 uint64_t head_dim, uint64_t length) {
     if (!heads_ok("attention_scores", q_heads, kv_heads, head_dim, 1)) return;
     Geom G = geom(kSingle, q_heads, kv_heads, head_dim);
     G.length = length;
@@ -519,21 +514,8 @@ SILVANN_EXPORT void silvann_gfx950_attention_scores(float* p, const uint16_t* q,
     check_launch("attention_scores");
 }
 
-// gpu.cuh:120 — kernels.cuh:1156-1164
-SILVANN_EXPORT void silvann_gfx950_attention_mix(uint16_t* o, const float* p, const uint16_t* v, uint64_t q_heads,
-                                                 uint64_t kv_heads, uint64_t head_dim, uint64_t length,
-                                                 unsigned int* over) {
-    if (!heads_ok("attention_mix", q_heads, kv_heads, head_dim, 1)) return;
-    Geom G = geom(kSingle, q_heads, kv_heads, head_dim);
-    G.length = length;
-    launch_mix(o, nullptr, p, v, G, 1, over);
-    check_launch("attention_mix");
-}
-
-// gpu.cuh:122 — kernels.cuh:1190-1221
-SILVANN_EXPORT void silvann_gfx950_attention_weights(float* p, float* res, const uint16_t* q, const uint16_t* k,
-                                                     uint64_t q_heads, uint64_t kv_heads, uint64_t head_dim,
-                                                     uint64_t length) {
+void weights_body(float* p, float* res, const uint16_t* q, const uint16_t* k, uint64_t q_heads, uint64_t kv_heads,
+                  uint64_t head_dim, uint64_t length) {
     if (!heads_ok("attention_weights", q_heads, kv_heads, head_dim, 1)) return;
     Geom G = geom(kSingle, q_heads, kv_heads, head_dim);
     G.length = length;
@@ -542,10 +524,121 @@ SILVANN_EXPORT void silvann_gfx950_attention_weights(float* p, float* res, const
     check_launch("attention_weights");
 }
 
+void causal_scores_grouped_body(float* p, const uint16_t* q, const uint16_t* k, uint64_t q_heads, uint64_t kv_heads,
+                                uint64_t head_dim, uint64_t first, uint64_t rows) {
+    if (!heads_ok("attention_causal_scores_grouped", q_heads, kv_heads, head_dim, rows)) return;
+    Geom G = geom(kCausal, q_heads, kv_heads, head_dim);
+    G.first = first;
+    G.span = first + rows;
+    launch_scores(p, q, k, G, rows, first + rows);
+    check_launch("attention_causal_scores_grouped");
+}
+
+void causal_softmax_body(float* p, uint64_t q_heads, uint64_t first, uint64_t rows) {
+    if (q_heads == 0) return;
+    Geom G = geom(kCausal, q_heads, 1, 1);
+    G.first = first;
+    G.span = first + rows;
+    launch_softmax(p, nullptr, G, rows * q_heads);
+    check_launch("attention_causal_softmax");
+}
+
+// A door records its chain's first step only when a fused form could take the chain (and the shape is valid:
+// an invalid one runs at once, to be refused).
+bool decode_chain_shape(uint64_t q_heads, uint64_t kv_heads, uint64_t head_dim, uint64_t length) {
+    return (head_dim == 64 || head_dim == 128 || head_dim == 256 || head_dim == 512) && kv_heads > 0 &&
+           q_heads > 0 && q_heads % kv_heads == 0 && length > 0 && length < (1ull << 31);
+}
+
+}  // namespace
+
+void flush_deferred() {
+    Deferred& d = deferred();
+    if (d.kind == kDeferNone) return;
+    const Deferred r = d;
+    d = Deferred();
+    switch (r.kind) {
+        case kDeferScores: scores_body(r.p, r.q, r.k, r.q_heads, r.kv_heads, r.head_dim, r.length); break;
+        case kDeferWeights: weights_body(r.p, r.res, r.q, r.k, r.q_heads, r.kv_heads, r.head_dim, r.length); break;
+        case kDeferCausal:
+            causal_scores_grouped_body(r.p, r.q, r.k, r.q_heads, r.kv_heads, r.head_dim, r.first, r.rows);
+            break;
+        case kDeferCausalSoftmax:
+            causal_scores_grouped_body(r.p, r.q, r.k, r.q_heads, r.kv_heads, r.head_dim, r.first, r.rows);
+            causal_softmax_body(r.p, r.q_heads, r.first, r.rows);
+            break;
+        default: break;
+    }
+}
+
+}  // namespace silvann
+
+using namespace silvann;
+
+// gpu.cuh:119 — kernels.cuh:1133-1141
+// Deferred when it may be a chain's first step (see common.hpp); its mix then runs the split-K decode.
+SILVANN_EXPORT void silvann_gfx950_attention_scores(float* p, const uint16_t* q, const uint16_t* k, uint64_t q_heads,
+                                                    uint64_t kv_heads, uint64_t head_dim, uint64_t length) {
+    flush_deferred();
+    if (defer_enabled() && decode_chain_shape(q_heads, kv_heads, head_dim, length)) {
+        Deferred& d = deferred();
+        d.kind = kDeferScores; d.p = p; d.q = q; d.k = k;
+        d.q_heads = q_heads; d.kv_heads = kv_heads; d.head_dim = head_dim; d.length = length; d.st = stream();
+        return;
+    }
+    scores_body(p, q, k, q_heads, kv_heads, head_dim, length);
+}
+
+// gpu.cuh:120 — kernels.cuh:1156-1164
+SILVANN_EXPORT void silvann_gfx950_attention_mix(uint16_t* o, const float* p, const uint16_t* v, uint64_t q_heads,
+                                                 uint64_t kv_heads, uint64_t head_dim, uint64_t length,
+                                                 unsigned int* over) {
+    Deferred& d = deferred();
+    if (d.kind == kDeferScores && d.p == p && d.q_heads == q_heads && d.kv_heads == kv_heads &&
+        d.head_dim == head_dim && d.length == length && d.st == stream() &&
+        decode_one(o, nullptr, d.q, d.k, v, q_heads, kv_heads, head_dim, length, (void*)p,
+                   q_heads * length * sizeof(float), over)) {
+        d = Deferred();   // the chain ran fused: p holds the splits' residuals, not weights
+        check_launch("attention_mix");
+        return;
+    }
+    flush_deferred();
+    if (!heads_ok("attention_mix", q_heads, kv_heads, head_dim, 1)) return;
+    Geom G = geom(kSingle, q_heads, kv_heads, head_dim);
+    G.length = length;
+    launch_mix(o, nullptr, p, v, G, 1, over);
+    check_launch("attention_mix");
+}
+
+// gpu.cuh:122 — kernels.cuh:1190-1221
+// Deferred when it may be a chain's first step; its residual_mix then runs the split-K decode into `res`.
+SILVANN_EXPORT void silvann_gfx950_attention_weights(float* p, float* res, const uint16_t* q, const uint16_t* k,
+                                                     uint64_t q_heads, uint64_t kv_heads, uint64_t head_dim,
+                                                     uint64_t length) {
+    flush_deferred();
+    if (defer_enabled() && decode_chain_shape(q_heads, kv_heads, head_dim, length)) {
+        Deferred& d = deferred();
+        d.kind = kDeferWeights; d.p = p; d.res = res; d.q = q; d.k = k;
+        d.q_heads = q_heads; d.kv_heads = kv_heads; d.head_dim = head_dim; d.length = length; d.st = stream();
+        return;
+    }
+    weights_body(p, res, q, k, q_heads, kv_heads, head_dim, length);
+}
+
 // gpu.cuh:123 — kernels.cuh:1224-1238
 SILVANN_EXPORT void silvann_gfx950_attention_residual_mix(float* res, const float* p, const uint16_t* v,
                                                           uint64_t q_heads, uint64_t kv_heads, uint64_t head_dim,
                                                           uint64_t length) {
+    Deferred& d = deferred();
+    if (d.kind == kDeferWeights && d.p == p && d.res == res && d.q_heads == q_heads && d.kv_heads == kv_heads &&
+        d.head_dim == head_dim && d.length == length && d.st == stream() &&
+        decode_one(nullptr, res, d.q, d.k, v, q_heads, kv_heads, head_dim, length, (void*)p,
+                   q_heads * length * sizeof(float), nullptr)) {
+        d = Deferred();
+        check_launch("attention_residual_mix");
+        return;
+    }
+    flush_deferred();
     if (!heads_ok("attention_residual_mix", q_heads, kv_heads, head_dim, 1)) return;
     Geom G = geom(kSingle, q_heads, kv_heads, head_dim);
     G.length = length;
@@ -556,6 +649,7 @@ SILVANN_EXPORT void silvann_gfx950_attention_residual_mix(float* res, const floa
 // gpu.cuh:124 — kernels.cuh:1243-1255
 SILVANN_EXPORT void silvann_gfx950_attention_merge(float* into, const float* a, const float* b, uint64_t q_heads,
                                                    uint64_t head_dim) {
+    silvann::flush_deferred();
     if (q_heads == 0) return;
     merge_heads<<<(uint32_t)((q_heads + 63) / 64), 64, 0, stream()>>>(into, a, b, q_heads, head_dim);
     check_launch("attention_merge");
@@ -564,6 +658,7 @@ SILVANN_EXPORT void silvann_gfx950_attention_merge(float* into, const float* a, 
 // gpu.cuh:125 — kernels.cuh:1258-1267
 SILVANN_EXPORT void silvann_gfx950_attention_finish(uint16_t* o, const float* res, uint64_t q_heads,
                                                     uint64_t head_dim, unsigned int* over) {
+    silvann::flush_deferred();
     const uint64_t n = q_heads * head_dim;
     if (n == 0) return;
     finish_heads<<<(uint32_t)((n + 255) / 256), 256, 0, stream()>>>(o, res, q_heads, head_dim, over);
@@ -574,6 +669,7 @@ SILVANN_EXPORT void silvann_gfx950_attention_finish(uint16_t* o, const float* re
 SILVANN_EXPORT void silvann_gfx950_attention_causal_scores(float* p, const uint16_t* q, const uint16_t* k,
                                                            uint64_t q_heads, uint64_t kv_heads, uint64_t head_dim,
                                                            uint64_t first, uint64_t rows) {
+    silvann::flush_deferred();
     if (!heads_ok("attention_causal_scores", q_heads, kv_heads, head_dim, rows)) return;
     Geom G = geom(kCausal, q_heads, kv_heads, head_dim);
     G.first = first;
@@ -587,6 +683,16 @@ SILVANN_EXPORT void silvann_gfx950_attention_causal_scores(float* p, const uint1
 SILVANN_EXPORT void silvann_gfx950_attention_causal_mix(uint16_t* o, const float* p, const uint16_t* v,
                                                         uint64_t q_heads, uint64_t kv_heads, uint64_t head_dim,
                                                         uint64_t first, uint64_t rows, unsigned int* over) {
+    Deferred& d = deferred();
+    if (d.kind == kDeferCausalSoftmax && d.p == p && d.q_heads == q_heads && d.kv_heads == kv_heads &&
+        d.head_dim == head_dim && d.first == first && d.rows == rows && d.st == stream()) {
+        const Deferred r = d;
+        d = Deferred();   // the chain runs fused: p is never written
+        causal_paged_launch(o, nullptr, r.q, r.k, v, nullptr, 0, q_heads, kv_heads, head_dim, first, rows, over,
+                            "attention_causal_mix");
+        return;
+    }
+    flush_deferred();
     if (!heads_ok("attention_causal_mix", q_heads, kv_heads, head_dim, rows)) return;
     Geom G = geom(kCausal, q_heads, kv_heads, head_dim);
     G.first = first;
@@ -599,6 +705,7 @@ SILVANN_EXPORT void silvann_gfx950_attention_causal_mix(uint16_t* o, const float
 SILVANN_EXPORT void silvann_gfx950_attention_scores_grouped(float* p, const uint16_t* q, const uint16_t* k,
                                                             uint64_t q_heads, uint64_t kv_heads, uint64_t head_dim,
                                                             uint64_t length) {
+    silvann::flush_deferred();
     if (!heads_ok("attention_scores_grouped", q_heads, kv_heads, head_dim, 1)) return;
     Geom G = geom(kSingle, q_heads, kv_heads, head_dim);
     G.length = length;
@@ -608,6 +715,7 @@ SILVANN_EXPORT void silvann_gfx950_attention_scores_grouped(float* p, const uint
 
 // gpu.cuh:190 — kernels.cuh:1095-1097
 SILVANN_EXPORT void silvann_gfx950_attention_softmax_rows(float* p, uint64_t rows, uint64_t length) {
+    silvann::flush_deferred();
     Geom G = geom(kSingle, 1, 1, 1);   // row r at r·length, `length` long: the one-query geometry
     G.length = length;
     if (length == 0) return;
@@ -616,31 +724,38 @@ SILVANN_EXPORT void silvann_gfx950_attention_softmax_rows(float* p, uint64_t row
 }
 
 // gpu.cuh:191 — kernels.cuh:1028-1061
+// Deferred when it may be a chain's first step; its causal_softmax and causal_mix then run causal_mfma.
 SILVANN_EXPORT void silvann_gfx950_attention_causal_scores_grouped(float* p, const uint16_t* q, const uint16_t* k,
                                                                    uint64_t q_heads, uint64_t kv_heads,
                                                                    uint64_t head_dim, uint64_t first, uint64_t rows) {
-    if (!heads_ok("attention_causal_scores_grouped", q_heads, kv_heads, head_dim, rows)) return;
-    Geom G = geom(kCausal, q_heads, kv_heads, head_dim);
-    G.first = first;
-    G.span = first + rows;
-    launch_scores(p, q, k, G, rows, first + rows);
-    check_launch("attention_causal_scores_grouped");
+    flush_deferred();
+    if (defer_enabled() && causal_shape_ok(q_heads, kv_heads, head_dim, first, rows, false, 0)) {
+        Deferred& d = deferred();
+        d.kind = kDeferCausal; d.p = p; d.q = q; d.k = k;
+        d.q_heads = q_heads; d.kv_heads = kv_heads; d.head_dim = head_dim; d.first = first; d.rows = rows;
+        d.st = stream();
+        return;
+    }
+    causal_scores_grouped_body(p, q, k, q_heads, kv_heads, head_dim, first, rows);
 }
 
 // gpu.cuh:192 — kernels.cuh:1065-1081
 SILVANN_EXPORT void silvann_gfx950_attention_causal_softmax(float* p, uint64_t q_heads, uint64_t first, uint64_t rows) {
-    if (q_heads == 0) return;
-    Geom G = geom(kCausal, q_heads, 1, 1);
-    G.first = first;
-    G.span = first + rows;
-    launch_softmax(p, nullptr, G, rows * q_heads);
-    check_launch("attention_causal_softmax");
+    Deferred& d = deferred();
+    if (d.kind == kDeferCausal && d.p == p && d.q_heads == q_heads && d.first == first && d.rows == rows &&
+        d.st == stream()) {
+        d.kind = kDeferCausalSoftmax;   // the chain's second step, recorded too
+        return;
+    }
+    flush_deferred();
+    causal_softmax_body(p, q_heads, first, rows);
 }
 
 // gpu.cuh:195 — doors.cuh:417-424
 SILVANN_EXPORT void silvann_gfx950_attention_weights_rows(float* p, float* res, const uint16_t* q, const uint16_t* k,
                                                           uint64_t q_heads, uint64_t kv_heads, uint64_t head_dim,
                                                           uint64_t first, uint64_t rows) {
+    silvann::flush_deferred();
     if (!heads_ok("attention_weights_rows", q_heads, kv_heads, head_dim, rows)) return;
     Geom G = geom(kByRow, q_heads, kv_heads, head_dim);
     G.first = first;
@@ -654,6 +769,7 @@ SILVANN_EXPORT void silvann_gfx950_attention_weights_rows(float* p, float* res, 
 SILVANN_EXPORT void silvann_gfx950_attention_residual_mix_rows(float* res, const float* p, const uint16_t* v,
                                                                uint64_t q_heads, uint64_t kv_heads, uint64_t head_dim,
                                                                uint64_t first, uint64_t rows) {
+    silvann::flush_deferred();
     if (!heads_ok("attention_residual_mix_rows", q_heads, kv_heads, head_dim, rows)) return;
     Geom G = geom(kByRow, q_heads, kv_heads, head_dim);
     G.first = first;
@@ -668,6 +784,7 @@ SILVANN_EXPORT void silvann_gfx950_attention_scores_grouped_rows(float* p, uint6
                                                                  const uint32_t* lens, uint64_t q_heads,
                                                                  uint64_t kv_heads, uint64_t head_dim, uint64_t most,
                                                                  uint64_t rows) {
+    silvann::flush_deferred();
     if (!heads_ok("attention_scores_grouped_rows", q_heads, kv_heads, head_dim, rows)) return;
     Geom G = geom(kLens, q_heads, kv_heads, head_dim);
     G.p_row = p_row; G.q_row = q_row; G.k_row = k_row; G.lens = lens;
@@ -678,6 +795,7 @@ SILVANN_EXPORT void silvann_gfx950_attention_scores_grouped_rows(float* p, uint6
 // gpu.cuh:223 — kernels.cuh:1104-1110
 SILVANN_EXPORT void silvann_gfx950_attention_softmax_lens(float* p, uint64_t p_row, const uint32_t* lens,
                                                           uint64_t heads, uint64_t rows) {
+    silvann::flush_deferred();
     if (heads == 0) return;
     Geom G = geom(kLens, heads, 1, 1);
     G.p_row = p_row; G.lens = lens;
@@ -690,6 +808,7 @@ SILVANN_EXPORT void silvann_gfx950_attention_mix_rows(uint16_t* o, uint64_t o_ro
                                                       const uint16_t* v, uint64_t v_row, const uint32_t* lens,
                                                       uint64_t q_heads, uint64_t kv_heads, uint64_t head_dim,
                                                       uint64_t rows, unsigned int* over) {
+    silvann::flush_deferred();
     if (!heads_ok("attention_mix_rows", q_heads, kv_heads, head_dim, rows)) return;
     Geom G = geom(kLens, q_heads, kv_heads, head_dim);
     G.p_row = p_row; G.k_row = v_row; G.o_row = o_row; G.lens = lens;
@@ -701,6 +820,7 @@ SILVANN_EXPORT void silvann_gfx950_attention_mix_rows(uint16_t* o, uint64_t o_ro
 SILVANN_EXPORT void silvann_gfx950_attention_weights_tq(float* p, float* res, const uint16_t* q, const uint8_t* codes,
                                                         const uint16_t* scales, uint64_t q_heads, uint64_t kv_heads,
                                                         uint64_t head_dim, uint64_t length, uint64_t d) {
+    silvann::flush_deferred();
     if (!heads_ok("attention_weights_tq", q_heads, kv_heads, head_dim, 1) ||
         !tq_ok("attention_weights_tq", codes, head_dim, d))
         return;
@@ -717,6 +837,7 @@ SILVANN_EXPORT void silvann_gfx950_attention_residual_mix_tq(float* res, const f
                                                              const uint16_t* scales, uint64_t q_heads,
                                                              uint64_t kv_heads, uint64_t head_dim, uint64_t length,
                                                              uint64_t d) {
+    silvann::flush_deferred();
     if (!heads_ok("attention_residual_mix_tq", q_heads, kv_heads, head_dim, 1) ||
         !tq_ok("attention_residual_mix_tq", codes, head_dim, d))
         return;
@@ -731,6 +852,7 @@ SILVANN_EXPORT void silvann_gfx950_attention_weights_tq_rows(float* p, float* re
                                                              const uint8_t* codes, const uint16_t* scales,
                                                              uint64_t q_heads, uint64_t kv_heads, uint64_t head_dim,
                                                              uint64_t length, uint64_t d, uint64_t rows) {
+    silvann::flush_deferred();
     if (!heads_ok("attention_weights_tq_rows", q_heads, kv_heads, head_dim, rows) ||
         !tq_ok("attention_weights_tq_rows", codes, head_dim, d))
         return;
@@ -748,6 +870,7 @@ SILVANN_EXPORT void silvann_gfx950_attention_residual_mix_tq_rows(float* res, co
                                                                   const uint16_t* scales, uint64_t q_heads,
                                                                   uint64_t kv_heads, uint64_t head_dim,
                                                                   uint64_t length, uint64_t d, uint64_t rows) {
+    silvann::flush_deferred();
     if (!heads_ok("attention_residual_mix_tq_rows", q_heads, kv_heads, head_dim, rows) ||
         !tq_ok("attention_residual_mix_tq_rows", codes, head_dim, d))
         return;

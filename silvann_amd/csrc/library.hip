@@ -1,6 +1,7 @@
 // library.hip — the library's control entry points: which stream a thread's doors are queued on, the
 // remembered launch failure, and the build's name.
 #include <stdio.h>
+#include <stdlib.h>
 #include <string.h>
 
 #include <atomic>
@@ -74,11 +75,34 @@ void refuse(const char* what) {
     mark_failed();
 }
 
+static thread_local Deferred tls_deferred;
+Deferred& deferred() { return tls_deferred; }
+
+// On unless SILVANN_GFX950_DEFER=0 (read once a process); each thread may switch its own.
+static bool defer_default() {
+    static const bool on = [] {
+        const char* e = getenv("SILVANN_GFX950_DEFER");
+        return !(e && strcmp(e, "0") == 0);
+    }();
+    return on;
+}
+static thread_local int tls_defer = -1;   // -1: the process default
+bool defer_enabled() { return tls_defer < 0 ? defer_default() : tls_defer != 0; }
+
 }  // namespace silvann
 
-SILVANN_EXPORT void silvann_gfx950_set_stream(void* s) { silvann::tls_stream = (hipStream_t)s; }
+SILVANN_EXPORT void silvann_gfx950_set_stream(void* s) {
+    silvann::flush_deferred();   // what is recorded runs on the stream it was recorded on
+    silvann::tls_stream = (hipStream_t)s;
+}
 SILVANN_EXPORT void* silvann_gfx950_get_stream(void) { return (void*)silvann::tls_stream; }
+SILVANN_EXPORT void silvann_gfx950_flush(void) { silvann::flush_deferred(); }
+SILVANN_EXPORT void silvann_gfx950_set_defer(int on) {
+    silvann::flush_deferred();
+    silvann::tls_defer = on != 0;
+}
 SILVANN_EXPORT int silvann_gfx950_launch_failed(void) {
+    silvann::flush_deferred();
     int d = -1;
     if (hipGetDevice(&d) != hipSuccess || d < 0 || d >= silvann::kDevicesSeen) return 0;
     return silvann::failed[d].exchange(0);

@@ -818,14 +818,19 @@ static bool prefill_pipe() {
     return on;
 }
 
+// The shapes causal_mfma takes (pages NULL or `page_size` positions a page).
+bool causal_shape_ok(uint64_t q_heads, uint64_t kv_heads, uint64_t head_dim, uint64_t first, uint64_t rows,
+                     bool paged, uint64_t page_size) {
+    return (head_dim == 64 || head_dim == 128 || head_dim == 256) && kv_heads > 0 && q_heads % kv_heads == 0 &&
+           rows > 0 && first + rows < (1ull << 31) &&
+           (!paged || (page_size > 0 && page_size < (1ull << 31) && page_size % kKT == 0));
+}
+
 // o (with over) for the fp16 answers, or res for the residuals; what = the entry point's name
 void causal_paged_launch(uint16_t* o, float* res, const uint16_t* q, const uint16_t* k, const uint16_t* v,
                          const uint32_t* pages, uint64_t page_size, uint64_t q_heads, uint64_t kv_heads,
                          uint64_t head_dim, uint64_t first, uint64_t rows, unsigned int* over, const char* what) {
-    const bool ok = (head_dim == 64 || head_dim == 128 || head_dim == 256) && kv_heads > 0 && q_heads % kv_heads == 0 &&
-                    rows > 0 && first + rows < (1ull << 31) &&
-                    (!pages || (page_size > 0 && page_size < (1ull << 31) && page_size % kKT == 0));
-    if (!ok) {
+    if (!causal_shape_ok(q_heads, kv_heads, head_dim, first, rows, pages != nullptr, page_size)) {
         refuse(what);
         return;
     }
@@ -896,6 +901,7 @@ SILVANN_EXPORT void silvann_gfx950_attention_causal_paged(uint16_t* o, const uin
                                                           const uint16_t* v, const uint32_t* pages, uint64_t page_size,
                                                           uint64_t q_heads, uint64_t kv_heads, uint64_t head_dim,
                                                           uint64_t first, uint64_t rows, unsigned int* over) {
+    silvann::flush_deferred();
     silvann::causal_paged_launch(o, nullptr, q, k, v, pages, page_size, q_heads, kv_heads, head_dim, first, rows, over,
                                  "attention_causal_paged");
 }
@@ -905,6 +911,7 @@ SILVANN_EXPORT void silvann_gfx950_attention_causal_residual_paged(float* res, c
                                                                    uint64_t page_size, uint64_t q_heads,
                                                                    uint64_t kv_heads, uint64_t head_dim, uint64_t first,
                                                                    uint64_t rows) {
+    silvann::flush_deferred();
     if (!res) {
         silvann::refuse("attention_causal_residual_paged");
         return;

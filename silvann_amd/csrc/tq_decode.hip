@@ -336,6 +336,7 @@ SILVANN_EXPORT void silvann_gfx950_attention_residual_tq(float* res, const uint1
                                                          const uint16_t* v_scales, uint64_t q_heads,
                                                          uint64_t kv_heads, uint64_t head_dim, uint64_t length,
                                                          uint64_t d, uint64_t rows, float* scratch) {
+    silvann::flush_deferred();
     silvann::residual_tq_launch(res, q, k_codes, k_scales, v_codes, v_scales, q_heads, kv_heads, head_dim, length, d,
                                 rows, scratch);
 }

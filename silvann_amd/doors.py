@@ -66,6 +66,16 @@ def set_stream(stream) -> None:
     _lib.lib().silvann_gfx950_set_stream(raw)
 
 
+def flush() -> None:
+    """Run a deferred chain door now (its weights are then in its buffer)."""
+    _lib.lib().silvann_gfx950_flush()
+
+
+def set_defer(on: bool) -> None:
+    """Deferral of chain doors on this thread (default on; SILVANN_GFX950_DEFER=0 makes off the default)."""
+    _lib.lib().silvann_gfx950_set_defer(1 if on else 0)
+
+
 def launch_failed() -> bool:
     return bool(_lib.lib().silvann_gfx950_launch_failed())
 

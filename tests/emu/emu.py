@@ -130,10 +130,11 @@ def run_cache_write(kc, vc, pages, pages_row, page_size, capacity, positions, ro
 
 def run_fp16(q, k, v, qh, kvh, hd, length=0, first=0, rows=0, timeout: int = 900):
     """attention_weights + attention_residual_mix over `length` keys (rows == 0), or their _rows forms for `rows`
-    rows from `first`: the weights, the residual after the first door and after the second."""
+    rows from `first`: the weights, the residual after the first door and after the second — each door on its own
+    (no deferred chain: the weights are read between the doors)."""
     many = rows > 0
     params = f"{'fp16_rows' if many else 'fp16'} {qh} {kvh} {hd} {first if many else length} {rows or 1} 0 0 0"
-    return _run({"q": q, "k": k, "v": v}, params, None, timeout,
+    return _run({"q": q, "k": k, "v": v}, params, {"SILVANN_GFX950_DEFER": "0"}, timeout,
                 outs=(("p", np.float32), ("res_w", np.float32), ("res", np.float32)))
 
 
@@ -153,3 +154,18 @@ def run_rope_rows(x, cs, rows, heads, head_stride, row_stride, rot, timeout: int
     """rope_rows in place on a copy of x (halves as uint16): the turned rows and the fault word."""
     params = f"rope {heads} 0 {head_stride} 0 {rows} {rot} 0 {row_stride}"
     return _run({"q": x, "k": cs}, params, None, timeout, outs=(("o", np.uint16),))
+
+
+def run_chain(kind, q, k, v, qh, kvh, hd, a0, a1=0, interleave=False, defer=True, timeout: int = 900):
+    """A reference verb's door chain through the library's doors: kind "decode" (scores, mix; a0 = length),
+    "weights" (weights, residual_mix; a0 = length) or "causal" (causal_scores_grouped, causal_softmax, causal_mix;
+    a0 = first, a1 = rows). `interleave` puts another door inside the chain; `defer` False runs every door on its
+    own. Answers the fp16 answers, the weights buffer afterwards, the residual (not for "causal") and the fault
+    word."""
+    env = None if defer else {"SILVANN_GFX950_DEFER": "0"}
+    if kind == "causal":
+        params = f"chain_causal {qh} {kvh} {hd} {a0} {a1} {1 if interleave else 0} 0 0"
+        return _run({"q": q, "k": k, "v": v}, params, env, timeout, outs=(("o", np.float16), ("p", np.float32)))
+    params = f"chain_{kind} {qh} {kvh} {hd} {a0} {1 if interleave else 0} 0 0 0"
+    return _run({"q": q, "k": k, "v": v}, params, env, timeout,
+                outs=(("o", np.float16), ("p", np.float32), ("res", np.float32)))

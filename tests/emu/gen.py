@@ -49,6 +49,12 @@ inline void check_launch(const char*) {}
 inline void prof_begin(int) {}
 inline void prof_end(int) {}
 inline void refuse(const char* what) { std::fprintf(stderr, "refused: %s\\n", what); emu_refused = 1; }
+// the deferral state of library.hip (not built here): on unless SILVANN_GFX950_DEFER=0
+inline Deferred& deferred() { static Deferred d; return d; }
+inline bool defer_enabled() {
+    const char* e = std::getenv("SILVANN_GFX950_DEFER");
+    return !(e && std::strcmp(e, "0") == 0);
+}
 }
 """
     return s

@@ -13,7 +13,12 @@
 #include "emu_rt.hpp"
 #include "silvann_gfx950_attention.h"
 
-namespace silvann { extern int emu_refused; }
+namespace silvann {
+extern int emu_refused;
+void flush_deferred();
+}
+// library.hip is not part of the emulation: its flush entry point, here
+extern "C" void silvann_gfx950_flush(void) { silvann::flush_deferred(); }
 
 namespace {
 struct Guarded { char* map; size_t len; char* p; size_t n; const char* name; };
@@ -162,6 +167,53 @@ int main(int argc, char** argv) {
         char* x = load(d + "/q.bin", "x", &xn);
         silvann_gfx950_rope_rows((uint16_t*)x, (const uint16_t*)x, (const float*)k, a1, qh, hd, k_row, ps, over);
         save(d + "/o.bin", x, xn);
+        save(d + "/over.bin", over, 4);
+        fprintf(stderr, "emu done: refused %d, wave exchanges %ld\n", silvann::emu_refused, (long)emu::ops);
+        return silvann::emu_refused ? 5 : 0;
+    } else if (std::string(mode) == "chain_decode" || std::string(mode) == "chain_weights") {
+        // The reference verbs' door chains over a0 = length keys, as the verbs call them (deferred unless
+        // SILVANN_GFX950_DEFER=0): scores then mix into o, or weights then residual_mix into res. a1 = 1 puts a
+        // merge of an unrelated pair of residuals between the two doors (which must run the first door as it was).
+        const unsigned long length = a0, rf = hd + 2;
+        float* p = (float*)guarded(qh * length * 4, "p");
+        memset(p, 0xFF, qh * length * 4);
+        float* res = (float*)guarded(qh * rf * 4, "res");
+        memset(res, 0xFF, qh * rf * 4);
+        float* other = (float*)guarded(2 * rf * 4, "other");
+        memset(other, 0, 2 * rf * 4);
+        const bool decode = std::string(mode) == "chain_decode";
+        const unsigned long on = qh * hd * 2;
+        uint16_t* o16 = (uint16_t*)guarded(on, "o");
+        memset(o16, 0xFF, on);
+        if (decode) silvann_gfx950_attention_scores(p, (const uint16_t*)q, (const uint16_t*)k, qh, kvh, hd, length);
+        else silvann_gfx950_attention_weights(p, res, (const uint16_t*)q, (const uint16_t*)k, qh, kvh, hd, length);
+        if (a1 == 1) silvann_gfx950_attention_merge(other, other, other + rf, 1, hd);
+        if (decode) silvann_gfx950_attention_mix(o16, p, (const uint16_t*)v, qh, kvh, hd, length, over);
+        else silvann_gfx950_attention_residual_mix(res, p, (const uint16_t*)v, qh, kvh, hd, length);
+        silvann_gfx950_flush();
+        save(d + "/o.bin", o16, on);
+        save(d + "/p.bin", p, qh * length * 4);
+        save(d + "/res.bin", res, qh * rf * 4);
+        save(d + "/over.bin", over, 4);
+        fprintf(stderr, "emu done: refused %d, wave exchanges %ld\n", silvann::emu_refused, (long)emu::ops);
+        return silvann::emu_refused ? 5 : 0;
+    } else if (std::string(mode) == "chain_causal") {
+        // causal_scores_grouped, causal_softmax, causal_mix from a0 = first over a1 = rows, as nn__attention__rows
+        // calls them; ps = 1 puts another door (a finish of nothing) between the softmax and the mix
+        const unsigned long first = a0, rows = a1, span = first + rows;
+        float* p = (float*)guarded(rows * qh * span * 4, "p");
+        memset(p, 0xFF, rows * qh * span * 4);
+        const unsigned long on = rows * qh * hd * 2;
+        uint16_t* o16 = (uint16_t*)guarded(on, "o");
+        memset(o16, 0xFF, on);
+        silvann_gfx950_attention_causal_scores_grouped(p, (const uint16_t*)q, (const uint16_t*)k, qh, kvh, hd, first,
+                                                       rows);
+        silvann_gfx950_attention_causal_softmax(p, qh, first, rows);
+        if (ps == 1) silvann_gfx950_attention_finish(nullptr, nullptr, 0, hd, over);
+        silvann_gfx950_attention_causal_mix(o16, p, (const uint16_t*)v, qh, kvh, hd, first, rows, over);
+        silvann_gfx950_flush();
+        save(d + "/o.bin", o16, on);
+        save(d + "/p.bin", p, rows * qh * span * 4);
         save(d + "/over.bin", over, 4);
         fprintf(stderr, "emu done: refused %d, wave exchanges %ld\n", silvann::emu_refused, (long)emu::ops);
         return silvann::emu_refused ? 5 : 0;

@@ -1,0 +1,82 @@
+"""Deferred door chains in the CPU emulation (tests/emu): the reference verbs' chains — attention_scores then
+attention_mix, attention_weights then attention_residual_mix, attention_causal_scores_grouped then
+attention_causal_softmax then attention_causal_mix — called through the library's doors as the verbs call them.
+
+- Deferred (the default) the chain runs fused, and the weights buffer shows it: untouched by the causal chain, the
+  split-K scratch (no weights) after the decode pairs; the answers meet the oracle at the fp16 bar, the residual
+  at tests/conftest.py::residual_parity's.
+- A pair too short for its splits to fit the weights buffer, another door inside the chain, and deferral switched
+  off all run each door on its own: the buffer then holds the oracle's weights.
+"""
+import numpy as np
+import pytest
+
+from tests.conftest import parity, residual_parity
+from tests.emu import emu
+
+pytestmark = pytest.mark.skipif(emu.compiler() is None, reason="no clang++ for the CPU emulation")
+
+
+def _inputs(seed, qh, kvh, hd, n, rows=1):
+    rng = np.random.default_rng(seed)
+    q = rng.standard_normal(rows * qh * hd).astype(np.float16)
+    k = rng.standard_normal(n * kvh * hd).astype(np.float16)
+    v = rng.standard_normal(n * kvh * hd).astype(np.float16)
+    return q, k, v
+
+
+@pytest.mark.parametrize("qh,kvh,hd,length,interleave,defer,fused", [
+    (16, 2, 256, 2048, False, True, True),    # fused: the splits fit the weights buffer
+    (16, 2, 256, 2048, True, True, False),    # another door between: each door on its own
+    (16, 2, 256, 2048, False, False, False),  # deferral off
+    (8, 2, 128, 40, False, True, False),      # too short for the splits to fit: each door on its own
+    (64, 1, 512, 700, False, True, True),     # one kv head, head_dim 512
+])
+def test_decode_pair(oracle, qh, kvh, hd, length, interleave, defer, fused):
+    q, k, v = _inputs(qh + hd + length, qh, kvh, hd, length)
+    o, p, _, over, _ = emu.run_chain("decode", q, k, v, qh, kvh, hd, length, interleave=interleave, defer=defer)
+    want_p = oracle.scores(q, k, qh, kvh, hd, length)
+    want_o, _ = oracle.mix(want_p, v, qh, kvh, hd, length)
+    parity(o, want_o)
+    assert over == 0
+    if fused:
+        assert not np.allclose(p, want_p, rtol=1e-4, atol=1e-6, equal_nan=False)
+    else:
+        np.testing.assert_allclose(p, want_p, rtol=1e-4, atol=1e-6)
+
+
+@pytest.mark.parametrize("qh,kvh,hd,length,interleave,fused", [
+    (16, 2, 128, 3000, False, True),
+    (16, 2, 128, 3000, True, False),
+])
+def test_weights_pair(oracle, qh, kvh, hd, length, interleave, fused):
+    q, k, v = _inputs(7 + length, qh, kvh, hd, length)
+    _, p, res, _, _ = emu.run_chain("weights", q, k, v, qh, kvh, hd, length, interleave=interleave)
+    wp, wres = oracle.weights(q, k, qh, kvh, hd, length)
+    wres = oracle.residual_mix(wres, wp, v, qh, kvh, hd, length)
+    residual_parity(res, wres, hd)
+    if fused:
+        assert not np.allclose(p, wp, rtol=1e-4, atol=1e-6)
+    else:
+        np.testing.assert_allclose(p, wp, rtol=1e-4, atol=1e-6)
+
+
+@pytest.mark.parametrize("qh,kvh,hd,first,rows,interleave,fused", [
+    (16, 2, 256, 77, 95, False, True),
+    (6, 3, 128, 10, 70, True, False),
+    (8, 1, 512, 5, 20, False, False),   # head_dim 512: no fused causal form, each door on its own
+])
+def test_causal_chain(oracle, qh, kvh, hd, first, rows, interleave, fused):
+    q, k, v = _inputs(first + rows, qh, kvh, hd, first + rows, rows)
+    o, p, over, _ = emu.run_chain("causal", q, k, v, qh, kvh, hd, first, rows, interleave=interleave)
+    want, _ = oracle.causal_rows(q, k, v, None, 0, qh, kvh, hd, first, list(range(rows)))
+    parity(o, want)
+    assert over == 0
+    if fused:
+        assert np.all(p.view(np.uint32) == 0xFFFFFFFF)   # the weights were never written
+    else:
+        wp = oracle.causal_softmax(oracle.causal_scores_grouped(q, k, qh, kvh, hd, first, rows), qh, first, rows)
+        # row r's weights are its first + r + 1 positions; past them the buffer keeps what it held
+        span = first + rows
+        valid = (np.arange(span)[None, :] <= first + np.repeat(np.arange(rows), qh)[:, None]).ravel()
+        np.testing.assert_allclose(p[valid], wp[valid], rtol=1e-4, atol=1e-6)

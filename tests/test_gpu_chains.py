@@ -1,0 +1,112 @@
+"""Deferred door chains on gfx950 (the same checks as tests/test_chains.py, on the GPU through the C ABI), at the
+BASELINE shapes: the reference's decode verb (attention_scores + attention_mix) over C1 and C5's caches, its
+residual verb (attention_weights + attention_residual_mix), and its rows verb (causal_scores_grouped +
+causal_softmax + causal_mix in passes) over C3's chunk — each fused, against the oracle at the fp16 bar; and the
+orders that must run each door on its own (another door inside the chain, a flush, a change of stream, deferral
+off), whose weights buffer then holds the oracle's weights.
+"""
+import numpy as np
+import pytest
+import torch
+
+from oracle.oracle import inputs
+from silvann_amd import doors, verbs
+from silvann_amd import workloads as W
+from tests.conftest import parity, residual_parity
+from tests.gpu_util import t
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(autouse=True)
+def deferral_on(dev):
+    doors.set_defer(True)
+    yield
+    doors.flush()
+
+
+def _z(dev, n, dtype=torch.float32):
+    return torch.zeros(n, dtype=dtype, device=dev)
+
+
+def _decode_case(seed, qh, kvh, hd, L):
+    return inputs(seed, (qh * hd,), (L * kvh * hd,), (L * kvh * hd,))
+
+
+@pytest.mark.parametrize("name,seed,qh,kvh,hd,L", [
+    ("C1", 1, 16, 2, 256, 2048),
+    ("C5", 5, 16, 2, 256, 262144),
+    ("mqa", 9, 32, 1, 128, 5000),
+])
+def test_decode_verb_runs_fused(dev, oracle, name, seed, qh, kvh, hd, L):
+    print(f"case: decode verb chain {name} qh{qh} kvh{kvh} hd{hd} L{L}", flush=True)
+    q, k, v = _decode_case(seed, qh, kvh, hd, L)
+    scores, out, over = _z(dev, qh * L), _z(dev, qh * hd, torch.float16), _z(dev, 1, torch.int32)
+    verbs.decode(t(q, dev), t(k, dev), t(v, dev), scores, out, qh, kvh, hd, 0, L, over)
+    want_p = oracle.scores(q, k, qh, kvh, hd, L)
+    want_o, _ = oracle.mix(want_p, v, qh, kvh, hd, L)
+    parity(out.cpu().numpy(), want_o)
+    assert int(over.item()) == 0
+    # fused: the scores buffer held the splits' scratch, never the weights
+    assert not np.allclose(scores.cpu().numpy(), want_p, rtol=1e-4, atol=1e-6)
+    assert not doors.launch_failed()
+
+
+def test_residual_verb_runs_fused(dev, oracle):
+    qh, kvh, hd, L = 16, 2, 128, 30000
+    print("case: residual verb chain", flush=True)
+    q, k, v = _decode_case(31, qh, kvh, hd, L)
+    scores, res = _z(dev, qh * L), _z(dev, qh * (hd + 2))
+    verbs.residual(t(q, dev), t(k, dev), t(v, dev), scores, res, qh, kvh, hd, 0, L)
+    wp, wres = oracle.weights(q, k, qh, kvh, hd, L)
+    wres = oracle.residual_mix(wres, wp, v, qh, kvh, hd, L)
+    residual_parity(res.cpu().numpy(), wres, hd)
+    assert not doors.launch_failed()
+
+
+def test_rows_verb_runs_fused(dev, oracle):
+    """C3's chunk through nn__attention__rows' attention part: passes of causal_scores_grouped, causal_softmax,
+    causal_mix, each pass one fused causal launch."""
+    w = W.config3()
+    print("case: rows verb chain C3", flush=True)
+    qh, kvh, hd, rows = w.q_heads, w.kv_heads, w.head_dim, w.rows
+    scores = _z(dev, 256 * qh * rows)   # room for passes of 256 rows
+    att = _z(dev, rows * qh * hd, torch.float16)
+    over = _z(dev, 1, torch.int32)
+    verbs.rows_attention(t(w.q, dev), t(w.k, dev), t(w.v, dev), scores, att, qh, kvh, hd, 0, rows, over)
+    which = [0, 1, 255, 256, 2047, rows - 1]
+    want, _ = oracle.causal_rows(w.q, w.k, w.v, None, 0, qh, kvh, hd, 0, which)
+    got = att.cpu().numpy().reshape(rows, qh * hd)[which].ravel()
+    parity(got, want)
+    assert int(over.item()) == 0
+    assert torch.count_nonzero(scores) == 0   # the weights were never written
+    assert not doors.launch_failed()
+
+
+@pytest.mark.parametrize("between", ["door", "flush", "stream", "off"])
+def test_orders_that_run_each_door_alone(dev, oracle, between):
+    qh, kvh, hd, L = 16, 2, 256, 2048
+    print(f"case: decode chain with {between} between", flush=True)
+    q, k, v = _decode_case(41, qh, kvh, hd, L)
+    scores, out, over = _z(dev, qh * L), _z(dev, qh * hd, torch.float16), _z(dev, 1, torch.int32)
+    if between == "off":
+        doors.set_defer(False)
+    doors.attention_scores(scores, t(q, dev), t(k, dev), qh, kvh, hd, L)
+    if between == "door":
+        r = _z(dev, 2 * (hd + 2))
+        doors.attention_merge(r, r, r[hd + 2:], 1, hd)
+    elif between == "flush":
+        doors.flush()
+    elif between == "stream":
+        s = torch.cuda.Stream()
+        doors.set_stream(s)
+        doors.set_stream(None)
+        s.synchronize()
+    want_p = oracle.scores(q, k, qh, kvh, hd, L)
+    torch.cuda.synchronize()
+    np.testing.assert_allclose(scores.cpu().numpy(), want_p, rtol=1e-5, atol=1e-7)
+    doors.attention_mix(out, scores, t(v, dev), qh, kvh, hd, L, over)
+    want_o, _ = oracle.mix(want_p, v, qh, kvh, hd, L)
+    parity(out.cpu().numpy(), want_o)
+    doors.set_defer(True)
+    assert not doors.launch_failed()

@@ -15,6 +15,15 @@ from tests.gpu_util import t
 
 pytestmark = pytest.mark.gpu
 
+
+@pytest.fixture(autouse=True)
+def each_door_on_its_own(dev):
+    """These tests read every door's buffers between doors, so no chain is deferred here (tests/test_gpu_chains.py
+    covers the deferred chains)."""
+    doors.set_defer(False)
+    yield
+    doors.set_defer(True)
+
 SHAPES = [(16, 2, 256, 333), (8, 8, 64, 65), (32, 4, 128, 1000), (64, 1, 128, 100), (6, 2, 72, 50),
           (6, 3, 9, 41)]   # an odd head_dim takes the dots' per-element arm (kernels.cuh:986-990)
 

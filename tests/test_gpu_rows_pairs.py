@@ -13,6 +13,15 @@ from tests.test_tq import make
 pytestmark = pytest.mark.gpu
 
 
+@pytest.fixture(autouse=True)
+def each_door_on_its_own(dev):
+    """These tests read every door's buffers between doors, so no chain is deferred here (tests/test_gpu_chains.py
+    covers the deferred chains)."""
+    doors.set_defer(False)
+    yield
+    doors.set_defer(True)
+
+
 def _z(dev, n, dtype=torch.float32):
     return torch.full((n,), float("nan"), dtype=dtype, device=dev)
 
