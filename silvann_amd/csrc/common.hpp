@@ -99,19 +99,26 @@ void refuse(const char* what);
 
 // ── deferred doors ──────────────────────────────────────────────────────────────────────────────────────
 // The reference's verbs call some doors only as chains, back to back on one thread: attention_scores then
-// attention_mix (attention__abi.cuh:155-158), attention_weights then attention_residual_mix (203-206), and
-// attention_causal_scores_grouped, attention_causal_softmax, attention_causal_mix (407-414). The first door of a
+// attention_mix (attention__abi.cuh:155-158), attention_weights then attention_residual_mix (203-206),
+// attention_causal_scores_grouped, attention_causal_softmax, attention_causal_mix (407-414), the TurboQuant pair
+// attention_weights_tq then attention_residual_mix_tq (266-269, mixer__abi.cuh:395-407), and the tiered prefill
+// window's many-row pairs (prefill__abi.cuh:430-440). The first door of a
 // chain is recorded, not launched; when its continuation arrives with the same operands the chain runs as one fused
 // kernel and the weights are never written. Any other door of this library first flushes what is recorded — runs
 // the recorded door as it would have run — so every other order keeps the reference's semantics.
-enum DeferKind : int { kDeferNone = 0, kDeferScores, kDeferWeights, kDeferCausal, kDeferCausalSoftmax };
+enum DeferKind : int {
+    kDeferNone = 0, kDeferScores, kDeferWeights, kDeferCausal, kDeferCausalSoftmax, kDeferWeightsRows, kDeferWeightsTq,
+    kDeferWeightsTqRows
+};
 struct Deferred {
     int kind = kDeferNone;
     float* p = nullptr;
     float* res = nullptr;
     const uint16_t* q = nullptr;
-    const uint16_t* k = nullptr;
-    uint64_t q_heads = 0, kv_heads = 0, head_dim = 0, length = 0, first = 0, rows = 0;
+    const uint16_t* k = nullptr;      // keys (fp16), or
+    const uint8_t* codes = nullptr;   // TurboQuant key codes
+    const uint16_t* scales = nullptr;
+    uint64_t q_heads = 0, kv_heads = 0, head_dim = 0, length = 0, first = 0, rows = 0, d = 0;
     hipStream_t st = nullptr;
 };
 Deferred& deferred();     // this thread's
@@ -120,6 +127,9 @@ void flush_deferred();    // launch what is recorded, if anything, and clear it
 // the fused forms the continuations launch (decode.hip, prefill.hip)
 bool decode_one(uint16_t* o, float* res, const uint16_t* q, const uint16_t* k, const uint16_t* v, uint64_t q_heads,
                 uint64_t kv_heads, uint64_t head_dim, uint64_t length, void* scratch, uint64_t cap, unsigned int* over);
+bool residual_tq_fit(float* res, const uint16_t* q, const uint8_t* kc, const uint16_t* ks, const uint8_t* vc,
+                     const uint16_t* vs, uint64_t q_heads, uint64_t kv_heads, uint64_t head_dim, uint64_t length,
+                     uint64_t d, uint64_t rows, void* scratch, uint64_t cap);
 bool causal_shape_ok(uint64_t q_heads, uint64_t kv_heads, uint64_t head_dim, uint64_t first, uint64_t rows,
                      bool paged, uint64_t page_size);
 void causal_paged_launch(uint16_t* o, float* res, const uint16_t* q, const uint16_t* k, const uint16_t* v,

@@ -543,6 +543,44 @@ void causal_softmax_body(float* p, uint64_t q_heads, uint64_t first, uint64_t ro
     check_launch("attention_causal_softmax");
 }
 
+void weights_rows_body(float* p, float* res, const uint16_t* q, const uint16_t* k, uint64_t q_heads, uint64_t kv_heads,
+                       uint64_t head_dim, uint64_t first, uint64_t rows) {
+    if (!heads_ok("attention_weights_rows", q_heads, kv_heads, head_dim, rows)) return;
+    Geom G = geom(kByRow, q_heads, kv_heads, head_dim);
+    G.first = first;
+    G.span = first + rows;
+    launch_scores(p, q, k, G, rows, first + rows);
+    launch_softmax(p, res, G, rows * q_heads);
+    check_launch("attention_weights_rows");
+}
+
+void weights_tq_body(float* p, float* res, const uint16_t* q, const uint8_t* codes, const uint16_t* scales,
+                     uint64_t q_heads, uint64_t kv_heads, uint64_t head_dim, uint64_t length, uint64_t d) {
+    if (!heads_ok("attention_weights_tq", q_heads, kv_heads, head_dim, 1) ||
+        !tq_ok("attention_weights_tq", codes, head_dim, d))
+        return;
+    Geom G = geom(kSingle, q_heads, kv_heads, head_dim);
+    G.length = length;
+    launch_tq_scores<kSingle>(p, q, codes, scales, G, 1, d);
+    launch_softmax(p, res, G, q_heads);
+    check_launch("attention_weights_tq");
+}
+
+void weights_tq_rows_body(float* p, float* res, const uint16_t* q, const uint8_t* codes, const uint16_t* scales,
+                          uint64_t q_heads, uint64_t kv_heads, uint64_t head_dim, uint64_t length, uint64_t d,
+                          uint64_t rows) {
+    if (!heads_ok("attention_weights_tq_rows", q_heads, kv_heads, head_dim, rows) ||
+        !tq_ok("attention_weights_tq_rows", codes, head_dim, d))
+        return;
+    Geom G = geom(kTqRows, q_heads, kv_heads, head_dim);
+    G.length = length;
+    launch_tq_scores<kTqRows>(p, q, codes, scales, G, rows, d);
+    Geom S = geom(kSingle, q_heads, kv_heads, head_dim);   // weight row i at i·length, its residual at i·(hd + 2)
+    S.length = length;
+    launch_softmax(p, res, S, rows * q_heads);
+    check_launch("attention_weights_tq_rows");
+}
+
 // A door records its chain's first step only when a fused form could take the chain (and the shape is valid:
 // an invalid one runs at once, to be refused).
 bool decode_chain_shape(uint64_t q_heads, uint64_t kv_heads, uint64_t head_dim, uint64_t length) {
@@ -566,6 +604,16 @@ void flush_deferred() {
         case kDeferCausalSoftmax:
             causal_scores_grouped_body(r.p, r.q, r.k, r.q_heads, r.kv_heads, r.head_dim, r.first, r.rows);
             causal_softmax_body(r.p, r.q_heads, r.first, r.rows);
+            break;
+        case kDeferWeightsRows:
+            weights_rows_body(r.p, r.res, r.q, r.k, r.q_heads, r.kv_heads, r.head_dim, r.first, r.rows);
+            break;
+        case kDeferWeightsTq:
+            weights_tq_body(r.p, r.res, r.q, r.codes, r.scales, r.q_heads, r.kv_heads, r.head_dim, r.length, r.d);
+            break;
+        case kDeferWeightsTqRows:
+            weights_tq_rows_body(r.p, r.res, r.q, r.codes, r.scales, r.q_heads, r.kv_heads, r.head_dim, r.length, r.d,
+                                 r.rows);
             break;
         default: break;
     }
@@ -755,21 +803,31 @@ SILVANN_EXPORT void silvann_gfx950_attention_causal_softmax(float* p, uint64_t q
 SILVANN_EXPORT void silvann_gfx950_attention_weights_rows(float* p, float* res, const uint16_t* q, const uint16_t* k,
                                                           uint64_t q_heads, uint64_t kv_heads, uint64_t head_dim,
                                                           uint64_t first, uint64_t rows) {
-    silvann::flush_deferred();
-    if (!heads_ok("attention_weights_rows", q_heads, kv_heads, head_dim, rows)) return;
-    Geom G = geom(kByRow, q_heads, kv_heads, head_dim);
-    G.first = first;
-    G.span = first + rows;
-    launch_scores(p, q, k, G, rows, first + rows);
-    launch_softmax(p, res, G, rows * q_heads);
-    check_launch("attention_weights_rows");
+    flush_deferred();
+    if (defer_enabled() && causal_shape_ok(q_heads, kv_heads, head_dim, first, rows, false, 0)) {
+        Deferred& d = deferred();   // with its residual_mix_rows: the causal residual (row 140)
+        d.kind = kDeferWeightsRows; d.p = p; d.res = res; d.q = q; d.k = k;
+        d.q_heads = q_heads; d.kv_heads = kv_heads; d.head_dim = head_dim; d.first = first; d.rows = rows;
+        d.st = stream();
+        return;
+    }
+    weights_rows_body(p, res, q, k, q_heads, kv_heads, head_dim, first, rows);
 }
 
 // gpu.cuh:196 — doors.cuh:425-432
 SILVANN_EXPORT void silvann_gfx950_attention_residual_mix_rows(float* res, const float* p, const uint16_t* v,
                                                                uint64_t q_heads, uint64_t kv_heads, uint64_t head_dim,
                                                                uint64_t first, uint64_t rows) {
-    silvann::flush_deferred();
+    Deferred& d = deferred();
+    if (d.kind == kDeferWeightsRows && d.p == p && d.res == res && d.q_heads == q_heads && d.kv_heads == kv_heads &&
+        d.head_dim == head_dim && d.first == first && d.rows == rows && d.st == stream()) {
+        const Deferred r = d;
+        d = Deferred();   // the pair runs fused: p is never written
+        causal_paged_launch(nullptr, res, r.q, r.k, v, nullptr, 0, q_heads, kv_heads, head_dim, first, rows, nullptr,
+                            "attention_residual_mix_rows");
+        return;
+    }
+    flush_deferred();
     if (!heads_ok("attention_residual_mix_rows", q_heads, kv_heads, head_dim, rows)) return;
     Geom G = geom(kByRow, q_heads, kv_heads, head_dim);
     G.first = first;
@@ -820,15 +878,15 @@ SILVANN_EXPORT void silvann_gfx950_attention_mix_rows(uint16_t* o, uint64_t o_ro
 SILVANN_EXPORT void silvann_gfx950_attention_weights_tq(float* p, float* res, const uint16_t* q, const uint8_t* codes,
                                                         const uint16_t* scales, uint64_t q_heads, uint64_t kv_heads,
                                                         uint64_t head_dim, uint64_t length, uint64_t d) {
-    silvann::flush_deferred();
-    if (!heads_ok("attention_weights_tq", q_heads, kv_heads, head_dim, 1) ||
-        !tq_ok("attention_weights_tq", codes, head_dim, d))
+    flush_deferred();
+    if (defer_enabled() && (d == 4 || d == 8)) {
+        Deferred& r = deferred();   // with its residual_mix_tq: the fused TurboQuant residual (row 139)
+        r.kind = kDeferWeightsTq; r.p = p; r.res = res; r.q = q; r.codes = codes; r.scales = scales;
+        r.q_heads = q_heads; r.kv_heads = kv_heads; r.head_dim = head_dim; r.length = length; r.d = d; r.rows = 1;
+        r.st = stream();
         return;
-    Geom G = geom(kSingle, q_heads, kv_heads, head_dim);
-    G.length = length;
-    launch_tq_scores<kSingle>(p, q, codes, scales, G, 1, d);
-    launch_softmax(p, res, G, q_heads);
-    check_launch("attention_weights_tq");
+    }
+    weights_tq_body(p, res, q, codes, scales, q_heads, kv_heads, head_dim, length, d);
 }
 
 // gpu.cuh:164 attention_residual_mix_tq — kernels.cuh:3005-3026. The weights are the pass's once read: its
@@ -837,7 +895,15 @@ SILVANN_EXPORT void silvann_gfx950_attention_residual_mix_tq(float* res, const f
                                                              const uint16_t* scales, uint64_t q_heads,
                                                              uint64_t kv_heads, uint64_t head_dim, uint64_t length,
                                                              uint64_t d) {
-    silvann::flush_deferred();
+    Deferred& r = deferred();
+    if (r.kind == kDeferWeightsTq && r.p == p && r.res == res && r.q_heads == q_heads && r.kv_heads == kv_heads &&
+        r.head_dim == head_dim && r.length == length && r.d == d && r.st == stream() &&
+        residual_tq_fit(res, r.q, r.codes, r.scales, codes, scales, q_heads, kv_heads, head_dim, length, d, 1,
+                        const_cast<float*>(p), q_heads * length * sizeof(float))) {
+        r = Deferred();   // the pair ran fused: p holds the splits' residuals, not weights
+        return;
+    }
+    flush_deferred();
     if (!heads_ok("attention_residual_mix_tq", q_heads, kv_heads, head_dim, 1) ||
         !tq_ok("attention_residual_mix_tq", codes, head_dim, d))
         return;
@@ -852,17 +918,15 @@ SILVANN_EXPORT void silvann_gfx950_attention_weights_tq_rows(float* p, float* re
                                                              const uint8_t* codes, const uint16_t* scales,
                                                              uint64_t q_heads, uint64_t kv_heads, uint64_t head_dim,
                                                              uint64_t length, uint64_t d, uint64_t rows) {
-    silvann::flush_deferred();
-    if (!heads_ok("attention_weights_tq_rows", q_heads, kv_heads, head_dim, rows) ||
-        !tq_ok("attention_weights_tq_rows", codes, head_dim, d))
+    flush_deferred();
+    if (defer_enabled() && (d == 4 || d == 8)) {
+        Deferred& r = deferred();   // with its residual_mix_tq_rows: row 139 over all the rows
+        r.kind = kDeferWeightsTqRows; r.p = p; r.res = res; r.q = q; r.codes = codes; r.scales = scales;
+        r.q_heads = q_heads; r.kv_heads = kv_heads; r.head_dim = head_dim; r.length = length; r.d = d; r.rows = rows;
+        r.st = stream();
         return;
-    Geom G = geom(kTqRows, q_heads, kv_heads, head_dim);
-    G.length = length;
-    launch_tq_scores<kTqRows>(p, q, codes, scales, G, rows, d);
-    Geom S = geom(kSingle, q_heads, kv_heads, head_dim);   // weight row i at i·length, its residual at i·(hd + 2)
-    S.length = length;
-    launch_softmax(p, res, S, rows * q_heads);
-    check_launch("attention_weights_tq_rows");
+    }
+    weights_tq_rows_body(p, res, q, codes, scales, q_heads, kv_heads, head_dim, length, d, rows);
 }
 
 // gpu.cuh:198 attention_residual_mix_tq_rows — doors.cuh:204,442-450
@@ -870,7 +934,15 @@ SILVANN_EXPORT void silvann_gfx950_attention_residual_mix_tq_rows(float* res, co
                                                                   const uint16_t* scales, uint64_t q_heads,
                                                                   uint64_t kv_heads, uint64_t head_dim,
                                                                   uint64_t length, uint64_t d, uint64_t rows) {
-    silvann::flush_deferred();
+    Deferred& r = deferred();
+    if (r.kind == kDeferWeightsTqRows && r.p == p && r.res == res && r.q_heads == q_heads && r.kv_heads == kv_heads &&
+        r.head_dim == head_dim && r.length == length && r.d == d && r.rows == rows && r.st == stream() &&
+        residual_tq_fit(res, r.q, r.codes, r.scales, codes, scales, q_heads, kv_heads, head_dim, length, d, rows,
+                        const_cast<float*>(p), rows * q_heads * length * sizeof(float))) {
+        r = Deferred();
+        return;
+    }
+    flush_deferred();
     if (!heads_ok("attention_residual_mix_tq_rows", q_heads, kv_heads, head_dim, rows) ||
         !tq_ok("attention_residual_mix_tq_rows", codes, head_dim, d))
         return;

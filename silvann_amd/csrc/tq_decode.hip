@@ -293,19 +293,16 @@ uint64_t residual_tq_scratch(uint64_t q_heads, uint64_t kv_heads, uint64_t head_
     return rows * q_heads * (nsplit > 0 ? nsplit : 1) * (head_dim + 2) * sizeof(float);
 }
 
-void residual_tq_launch(float* res, const uint16_t* q, const uint8_t* kc, const uint16_t* ks, const uint8_t* vc,
-                        const uint16_t* vs, uint64_t q_heads, uint64_t kv_heads, uint64_t head_dim, uint64_t length,
-                        uint64_t d, uint64_t rows, float* scratch) {
-    if (!tq_shape_ok(q_heads, kv_heads, head_dim, length, d, rows) || (((uintptr_t)kc | (uintptr_t)vc) & 7u) != 0) {
-        refuse("attention_residual_tq");
-        return;
-    }
+// The launch with a given split length (a multiple of the waves' tiles).
+void residual_tq_run(float* res, const uint16_t* q, const uint8_t* kc, const uint16_t* ks, const uint8_t* vc,
+                     const uint16_t* vs, uint64_t q_heads, uint64_t kv_heads, uint64_t head_dim, uint64_t length,
+                     uint64_t d, uint64_t rows, float* scratch, uint32_t chunk) {
     TqArgs a;
     a.q = q; a.kc = kc; a.ks = ks; a.vc = vc; a.vs = vs;
     a.q_heads = (uint32_t)q_heads; a.kv_heads = (uint32_t)kv_heads; a.group = (uint32_t)(q_heads / kv_heads);
     a.hblocks = tq_hblocks(q_heads, kv_heads);
     a.length = (uint32_t)length; a.rows = (uint32_t)rows;
-    a.chunk = tq_chunk(head_dim, kv_heads, a.hblocks, length, rows);
+    a.chunk = chunk;
     a.nsplit = (uint32_t)((length + a.chunk - 1) / a.chunk);
     a.row_bytes = (uint32_t)((head_dim + 16 / d - 1) / (16 / d) * 2);
     a.scale = 1.0f / sqrtf((float)head_dim);
@@ -327,6 +324,40 @@ void residual_tq_launch(float* res, const uint16_t* q, const uint8_t* kc, const 
         default: tq_merge<256><<<mgrid, 256, 0, st>>>(res, scratch, a.q_heads, a.nsplit); break;
     }
     check_launch("attention_residual_tq");
+}
+
+void residual_tq_launch(float* res, const uint16_t* q, const uint8_t* kc, const uint16_t* ks, const uint8_t* vc,
+                        const uint16_t* vs, uint64_t q_heads, uint64_t kv_heads, uint64_t head_dim, uint64_t length,
+                        uint64_t d, uint64_t rows, float* scratch) {
+    if (!tq_shape_ok(q_heads, kv_heads, head_dim, length, d, rows) || (((uintptr_t)kc | (uintptr_t)vc) & 7u) != 0) {
+        refuse("attention_residual_tq");
+        return;
+    }
+    residual_tq_run(res, q, kc, ks, vc, vs, q_heads, kv_heads, head_dim, length, d, rows, scratch,
+                    tq_chunk(head_dim, kv_heads, tq_hblocks(q_heads, kv_heads), length, rows));
+}
+
+// The deferred TurboQuant pairs' fused form: weights_tq(_rows) + residual_mix_tq(_rows) as row 139, its scratch the
+// pair's own weights buffer (`cap` bytes), the splits made long enough for their residuals to fit it. Answers false,
+// launching nothing, when the operands are not ones row 139 takes or no split length fits.
+bool residual_tq_fit(float* res, const uint16_t* q, const uint8_t* kc, const uint16_t* ks, const uint8_t* vc,
+                     const uint16_t* vs, uint64_t q_heads, uint64_t kv_heads, uint64_t head_dim, uint64_t length,
+                     uint64_t d, uint64_t rows, void* scratch, uint64_t cap) {
+    if (!tq_shape_ok(q_heads, kv_heads, head_dim, length, d, rows) || length == 0 ||
+        (((uintptr_t)kc | (uintptr_t)vc) & 7u) != 0 || (((uintptr_t)scratch) & 3u) != 0)
+        return false;
+    const uint64_t per_split = rows * q_heads * (head_dim + 2) * sizeof(float);
+    const uint64_t fit = cap / per_split;
+    if (fit == 0) return false;
+    const uint32_t hb = tq_hblocks(q_heads, kv_heads);
+    const uint64_t step = (uint64_t)tile_keys((int)head_dim) * kWaves;
+    uint64_t chunk = tq_chunk(head_dim, kv_heads, hb, length, rows);
+    if ((length + chunk - 1) / chunk > fit) chunk = ((length + fit - 1) / fit + step - 1) / step * step;
+    const uint64_t nsplit = (length + chunk - 1) / chunk;
+    if (nsplit > fit || nsplit > kMaxSplits) return false;
+    residual_tq_run(res, q, kc, ks, vc, vs, q_heads, kv_heads, head_dim, length, d, rows, (float*)scratch,
+                    (uint32_t)chunk);
+    return true;
 }
 
 }  // namespace silvann

@@ -105,10 +105,10 @@ def run_decode(w, env: dict | None = None, timeout: int = 900, shared: bool = Fa
 
 
 def run_tq(q, codes, scales, qh, kvh, hd, length, d, rows=0, timeout: int = 900):
-    """weights_tq then residual_mix_tq (their _rows forms when rows > 0): the weights and the residual after the
-    first door, and the residual after the second."""
+    """weights_tq then residual_mix_tq (their _rows forms when rows > 0), each door on its own: the weights and the
+    residual after the first door, and the residual after the second."""
     params = f"{'tq_rows' if rows else 'tq'} {qh} {kvh} {hd} {length} {max(rows, 1)} {d} 0 0"
-    return _run({"q": q, "k": codes, "v": scales}, params, None, timeout,
+    return _run({"q": q, "k": codes, "v": scales}, params, {"SILVANN_GFX950_DEFER": "0"}, timeout,
                 outs=(("p", np.float32), ("res_w", np.float32), ("res", np.float32)))
 
 
@@ -169,3 +169,16 @@ def run_chain(kind, q, k, v, qh, kvh, hd, a0, a1=0, interleave=False, defer=True
     params = f"chain_{kind} {qh} {kvh} {hd} {a0} {1 if interleave else 0} 0 0 0"
     return _run({"q": q, "k": k, "v": v}, params, env, timeout,
                 outs=(("o", np.float16), ("p", np.float32), ("res", np.float32)))
+
+
+def run_chain_residual(kind, q, kcodes, kscales, vcodes, vscales, qh, kvh, hd, a0, rows=1, d=0, interleave=False,
+                       defer=True, timeout: int = 900):
+    """The residual chains as the verbs call them: kind "rows" (weights_rows + residual_mix_rows from a0 = first over
+    `rows` rows; kcodes/vcodes are the fp16 keys and values), "tq" (weights_tq + residual_mix_tq over a0 = length
+    rows of width d) or "tq_rows" (their _rows forms for `rows` query rows). The weights buffer afterwards, the
+    residuals and the fault word."""
+    env = None if defer else {"SILVANN_GFX950_DEFER": "0"}
+    params = f"cres_{ {'rows': 'rows', 'tq': 'tq', 'tq_rows': 'tqr'}[kind]} {qh} {kvh} {hd} {a0} {rows} {d} " \
+             f"{1 if interleave else 0} 0"
+    files = {"q": q, "k": kcodes, "v": vcodes, "pages": kscales, "lens": vscales}
+    return _run(files, params, env, timeout, outs=(("p", np.float32), ("res", np.float32)))

@@ -197,6 +197,38 @@ int main(int argc, char** argv) {
         save(d + "/over.bin", over, 4);
         fprintf(stderr, "emu done: refused %d, wave exchanges %ld\n", silvann::emu_refused, (long)emu::ops);
         return silvann::emu_refused ? 5 : 0;
+    } else if (std::string(mode).rfind("cres_", 0) == 0) {
+        // the residual chains (a0 = first or length, a1 = rows, ps = d, pages_row = 1: another door in between);
+        // TurboQuant: k / v the codes, pages / lens the key / value scales
+        const std::string kind = std::string(mode).substr(5);   // rows, tq or tqr
+        const unsigned long rows = a1, rf = hd + 2, span = kind == "rows" ? a0 + a1 : a0;
+        float* p = (float*)guarded(rows * qh * span * 4, "p");
+        memset(p, 0xFF, rows * qh * span * 4);
+        float* res = (float*)guarded(rows * qh * rf * 4, "res");
+        memset(res, 0xFF, rows * qh * rf * 4);
+        char* vs = load(d + "/lens.bin", "v_scales");
+        if (kind == "rows")
+            silvann_gfx950_attention_weights_rows(p, res, (const uint16_t*)q, (const uint16_t*)k, qh, kvh, hd, a0, rows);
+        else if (kind == "tq")
+            silvann_gfx950_attention_weights_tq(p, res, (const uint16_t*)q, (const uint8_t*)k, (const uint16_t*)pages, qh,
+                                                kvh, hd, a0, ps);
+        else
+            silvann_gfx950_attention_weights_tq_rows(p, res, (const uint16_t*)q, (const uint8_t*)k,
+                                                     (const uint16_t*)pages, qh, kvh, hd, a0, ps, rows);
+        if (pages_row == 1) silvann_gfx950_attention_finish(nullptr, nullptr, 0, hd, over);
+        if (kind == "rows")
+            silvann_gfx950_attention_residual_mix_rows(res, p, (const uint16_t*)v, qh, kvh, hd, a0, rows);
+        else if (kind == "tq")
+            silvann_gfx950_attention_residual_mix_tq(res, p, (const uint8_t*)v, (const uint16_t*)vs, qh, kvh, hd, a0, ps);
+        else
+            silvann_gfx950_attention_residual_mix_tq_rows(res, p, (const uint8_t*)v, (const uint16_t*)vs, qh, kvh, hd, a0,
+                                                          ps, rows);
+        silvann_gfx950_flush();
+        save(d + "/p.bin", p, rows * qh * span * 4);
+        save(d + "/res.bin", res, rows * qh * rf * 4);
+        save(d + "/over.bin", over, 4);
+        fprintf(stderr, "emu done: refused %d, wave exchanges %ld\n", silvann::emu_refused, (long)emu::ops);
+        return silvann::emu_refused ? 5 : 0;
     } else if (std::string(mode) == "chain_causal") {
         // causal_scores_grouped, causal_softmax, causal_mix from a0 = first over a1 = rows, as nn__attention__rows
         // calls them; ps = 1 puts another door (a finish of nothing) between the softmax and the mix

@@ -80,3 +80,46 @@ def test_causal_chain(oracle, qh, kvh, hd, first, rows, interleave, fused):
         span = first + rows
         valid = (np.arange(span)[None, :] <= first + np.repeat(np.arange(rows), qh)[:, None]).ravel()
         np.testing.assert_allclose(p[valid], wp[valid], rtol=1e-4, atol=1e-6)
+
+
+@pytest.mark.parametrize("first,rows,interleave,fused", [(300, 40, False, True), (300, 40, True, False)])
+def test_weights_rows_pair(oracle, first, rows, interleave, fused):
+    """weights_rows + residual_mix_rows (the tiered prefill window's part 0) as the causal residual (row 140)."""
+    qh, kvh, hd = 16, 2, 256
+    q, k, v = _inputs(first + rows + 5, qh, kvh, hd, first + rows, rows)
+    p, res, _, _ = emu.run_chain_residual("rows", q, k, None, v, None, qh, kvh, hd, first, rows=rows,
+                                          interleave=interleave)
+    wp, wres = oracle.weights_rows(q, k, qh, kvh, hd, first, rows)
+    wres = oracle.residual_mix_rows(wres, wp, v, qh, kvh, hd, first, rows)
+    residual_parity(res, wres, hd)
+    if fused:
+        assert np.all(p.view(np.uint32) == 0xFFFFFFFF)
+    else:
+        assert not np.all(p.view(np.uint32) == 0xFFFFFFFF)
+
+
+@pytest.mark.parametrize("kind,d,hd,length,rows,interleave,fused", [
+    ("tq", 8, 128, 3000, 1, False, True),       # a tier's residual (the tiers' verbs)
+    ("tq", 4, 128, 3000, 1, True, False),
+    ("tq_rows", 4, 64, 2000, 3, False, True),   # the tiered prefill window's tier part
+])
+def test_tq_pair(oracle, kind, d, hd, length, rows, interleave, fused):
+    from tests.test_tq import header_levels, make
+    qh, kvh = 8, 2
+    rng = np.random.default_rng(d + hd + length + rows)
+    lev = header_levels(d)
+    q, kc, ks = make(rng, qh, kvh, hd, length, d, rows=rows)
+    _, vc, vs = make(rng, qh, kvh, hd, length, d)
+    p, res, _, _ = emu.run_chain_residual(kind, q, kc, ks, vc, vs, qh, kvh, hd, length, rows=rows, d=d,
+                                          interleave=interleave)
+    wp, wres = oracle.weights_tq_rows(q, kc, ks, qh, kvh, hd, length, d, rows, lev)
+    wres = oracle.residual_mix_tq_rows(wres, wp, vc, vs, qh, kvh, hd, length, d, rows, lev)
+    # the fused form's keys go through the matrix cores as fp16 (level · scale rounded): m to that rounding
+    w = hd + 2
+    g, o = res.reshape(-1, w).astype(np.float64), wres.reshape(-1, w).astype(np.float64)
+    np.testing.assert_allclose(g[:, 0], o[:, 0], rtol=0, atol=2e-3 * max(1.0, float(np.abs(o[:, 0]).max())))
+    at = np.exp(g[:, 0] - o[:, 0])[:, None]
+    np.testing.assert_allclose(g[:, 1:2] * at, o[:, 1:2], rtol=2e-3)
+    np.testing.assert_allclose(g[:, 2:] * at, o[:, 2:], rtol=0, atol=4e-3 * float(np.abs(o[:, 2:]).max()))
+    if not fused:   # each door on its own: the oracle's residual to the doors' own bar
+        np.testing.assert_allclose(res, wres, rtol=1e-4, atol=1e-5 * float(np.abs(wres).max()))

@@ -1,7 +1,8 @@
 """Deferred door chains on gfx950 (the same checks as tests/test_chains.py, on the GPU through the C ABI), at the
 BASELINE shapes: the reference's decode verb (attention_scores + attention_mix) over C1 and C5's caches, its
-residual verb (attention_weights + attention_residual_mix), and its rows verb (causal_scores_grouped +
-causal_softmax + causal_mix in passes) over C3's chunk — each fused, against the oracle at the fp16 bar; and the
+residual verb (attention_weights + attention_residual_mix), its rows verb (causal_scores_grouped + causal_softmax +
+causal_mix in passes) over C3's chunk and its tiers' verb (attention_weights_tq + attention_residual_mix_tq) — each
+fused, against the oracle at the fp16 bar (tests/test_gpu_window.py runs the window's many-row pairs); and the
 orders that must run each door on its own (another door inside the chain, a flush, a change of stream, deferral
 off), whose weights buffer then holds the oracle's weights.
 """
@@ -109,4 +110,29 @@ def test_orders_that_run_each_door_alone(dev, oracle, between):
     want_o, _ = oracle.mix(want_p, v, qh, kvh, hd, L)
     parity(out.cpu().numpy(), want_o)
     doors.set_defer(True)
+    assert not doors.launch_failed()
+
+
+@pytest.mark.parametrize("d,length", [(4, 70000), (8, 3000)])
+def test_tier_verb_runs_fused(dev, oracle, d, length):
+    """The tiers' verb (nn__attention__residual_tq: weights_tq then residual_mix_tq) as row 139, the weights buffer
+    its scratch."""
+    from tests.test_tq import header_levels, make
+    qh, kvh, hd = 16, 2, 256
+    print(f"case: tier verb chain d{d} length{length}", flush=True)
+    rng = np.random.default_rng(d + length)
+    lev = header_levels(d)
+    q, kc, ks = make(rng, qh, kvh, hd, length, d)
+    _, vc, vs = make(rng, qh, kvh, hd, length, d)
+    scores, res = _z(dev, 2 * qh * length), _z(dev, qh * (hd + 2))
+    verbs.residual_tq(t(q, dev), t(kc, dev), t(ks, dev), t(vc, dev), t(vs, dev), scores, res, qh, kvh, hd, d, length)
+    wp, wres = oracle.weights_tq(q, kc, ks, qh, kvh, hd, length, d, lev)
+    wres = oracle.residual_mix_tq(wres, wp, vc, vs, qh, kvh, hd, length, d, lev)
+    w = hd + 2
+    g, o = res.cpu().numpy().reshape(-1, w).astype(np.float64), wres.reshape(-1, w).astype(np.float64)
+    np.testing.assert_allclose(g[:, 0], o[:, 0], rtol=0, atol=2e-3 * max(1.0, float(np.abs(o[:, 0]).max())))
+    at = np.exp(g[:, 0] - o[:, 0])[:, None]
+    fin = lambda r: (r[:, 2:] / r[:, 1:2]).astype(np.float16)  # noqa: E731
+    np.testing.assert_allclose(g[:, 1:2] * at, o[:, 1:2], rtol=2e-3)
+    parity(fin(g), fin(o))
     assert not doors.launch_failed()

@@ -16,6 +16,15 @@ from tests.test_tq import header_levels, make
 pytestmark = pytest.mark.gpu
 
 
+@pytest.fixture(autouse=True)
+def each_door_on_its_own(dev):
+    """test_tq_doors reads the weights between the doors, so no pair is deferred here (tests/test_gpu_chains.py
+    covers the deferred pairs)."""
+    doors.set_defer(False)
+    yield
+    doors.set_defer(True)
+
+
 @pytest.mark.parametrize("d,hd,qh,kvh,length,rows", [
     (8, 128, 8, 2, 300, 0),
     (4, 256, 16, 2, 2500, 0),
