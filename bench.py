@@ -21,7 +21,8 @@ latent attention (64 heads over 131,072 512-wide latents, row 137 with k = v) in
 
 The TurboQuant, writer and latent lines run as child processes (`--only 6`..`9`), each under a time limit, so a
 failure there is recorded in its entry and cannot take the headline down; so does C2 once more with the split-K
-decode's fused finish (SILVANN_GFX950_DECODE_FUSED=1), the candidate for its default.
+decode's fused finish (SILVANN_GFX950_DECODE_FUSED=1), the candidate for its default, and C5 / C3 through the
+reference's own decode and rows verbs, whose door chains this library defers and runs fused.
 
 `cpu_baseline` is the reference's own x86_avx2 silicon family (oracle/_ref, built from the reference's
 sources) over the same batch, its doors called through its nn table on the host cores — both of the
@@ -59,7 +60,8 @@ def parse():
     ap.add_argument("--cpu-threads", type=int, default=int(os.environ.get("BENCH_CPU_THREADS", "16")))
     ap.add_argument("--only", type=int, default=0,
                     help="time only this config (1-5: BASELINE.json's; 6, 7: a 4-bit / 8-bit TurboQuant tier; 8: the "
-                         "cache writer on C4's chunk; 9: GLM 5.3's latent attention), no CPU leg")
+                         "cache writer on C4's chunk; 9: GLM 5.3's latent attention; 10, 11: C5 / C3 through the "
+                         "reference's own decode / rows verb), no CPU leg")
     ap.add_argument("--copy-probe", action="store_true",
                     help="run a plain 1 GiB device-to-device copy 5 times and exit: the known-size kernel the "
                          "FETCH_SIZE / WRITE_SIZE counters are scaled by")
@@ -203,6 +205,46 @@ def bench_latent(w, dev, steps, warmup):
     }, out
 
 
+def bench_verb(n, dev, steps, warmup):
+    """The reference's own verbs on this library's doors, no change to the caller: C5 through the decode verb
+    (attention_scores then attention_mix, a deferred chain run as the split-K decode), or C3 through the rows verb
+    (passes of causal_scores_grouped, causal_softmax, causal_mix, each run as the causal kernel). Wall-clock rate of
+    whole steps; the kernel timing is the fused kernel's."""
+    import torch
+    from silvann_amd import verbs
+    from silvann_amd import workloads as W
+    over = torch.zeros(1, dtype=torch.int32, device=dev)
+    if n == 10:
+        w = W.config5(dev=dev)
+        L = int(w.lens[0])
+        k, v = w.k, w.v
+        scores = torch.empty(w.q_heads * L, dtype=torch.float32, device=dev)
+        out = torch.empty(w.q_heads * w.head_dim, dtype=torch.float16, device=dev)
+
+        def step():
+            verbs.decode(w.q, k, v, scores, out, w.q_heads, w.kv_heads, w.head_dim, 0, L, over)
+        kernel, units = "decode_split", w.io_bytes()
+    else:
+        w = W.config3(dev=dev)
+        scores = torch.empty(256 * w.q_heads * w.rows, dtype=torch.float32, device=dev)
+        out = torch.empty(w.rows * w.q_heads * w.head_dim, dtype=torch.float16, device=dev)
+
+        def step():
+            verbs.rows_attention(w.q, w.k, w.v, scores, out, w.q_heads, w.kv_heads, w.head_dim, w.first, w.rows, over)
+        kernel, units = "causal_mfma", w.flops()
+    wall, kms, _ = time_steps(step, steps, warmup, kernel)
+    if int(over.item()):
+        raise RuntimeError(f"fault word {int(over.item()):#x}")
+    per_step_kernel_ms = kms   # average launch; the rows verb launches one a pass
+    if n == 10:
+        return {"config": "C5 through the decode verb (scores -> mix)", "unit": "GB/s",
+                "value": units * steps / wall / 1e9, "ms_per_step": wall / steps * 1e3, "bytes_per_step": units,
+                "split_ms": per_step_kernel_ms}, out
+    return {"config": "C3 through the rows verb (causal scores -> softmax -> mix, 256-row passes)", "unit": "TFLOP/s",
+            "value": units * steps / wall / 1e12, "ms_per_step": wall / steps * 1e3, "flops_per_step": units,
+            "kernel_ms_per_pass": per_step_kernel_ms}, out
+
+
 def bench_write(w, dev, steps, warmup):
     """The cache writer (attention_cache_write_paged): a chunk's keys turned and its keys and values placed in
     their pages, GB/s of rows read and written and angles read."""
@@ -312,6 +354,10 @@ def main():
         print(json.dumps({"copy_probe_bytes": src.numel() * 2, "launches": 5}), flush=True)
         return
 
+    if a.only in (10, 11):
+        r = bench_verb(a.only, dev, a.steps, a.warmup)[0]
+        print(json.dumps(r), flush=True)
+        return
     if a.only in W.LATENTS:
         r = bench_latent(W.LATENTS[a.only](dev=dev), dev, a.steps, a.warmup)[0]
         print(json.dumps(r), flush=True)
@@ -347,6 +393,8 @@ def main():
             secondary.append(isolated(n, max(5, a.steps // 2), a.warmup))
         secondary.append(isolated(2, a.steps, a.warmup, env={"SILVANN_GFX950_DECODE_FUSED": "1"},
                                   variant="fused finish (no merge launch)"))
+        for n in (10, 11):
+            secondary.append(isolated(n, max(5, a.steps // 2), a.warmup))
     cpu = None if a.no_cpu else cpu_baseline(w2, a.cpu_threads)
 
     line = {

@@ -8,6 +8,10 @@ carrying the word; nothing is launched.
 
 The two paged verbs are new (the reference has no page table): `decode_paged` and `causal_paged`, the
 split-K decode and the fused causal prefill, with the same kind of checks.
+
+The reference's verbs call their doors as chains (`decode`: scores then mix; `residual`: weights then residual_mix;
+`rows_attention`: causal scores, softmax, mix; `residual_tq`; the window's pairs); the library defers a chain's first
+door and runs the chain fused, so these verbs reach the fast kernels with the reference's own call sequence.
 """
 from __future__ import annotations
 
