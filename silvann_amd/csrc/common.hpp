@@ -127,6 +127,9 @@ void flush_deferred();    // launch what is recorded, if anything, and clear it
 // the fused forms the continuations launch (decode.hip, prefill.hip)
 bool decode_one(uint16_t* o, float* res, const uint16_t* q, const uint16_t* k, const uint16_t* v, uint64_t q_heads,
                 uint64_t kv_heads, uint64_t head_dim, uint64_t length, void* scratch, uint64_t cap, unsigned int* over);
+bool decode_causal(uint16_t* o, const uint16_t* q, const uint16_t* k, const uint16_t* v, uint64_t q_heads,
+                   uint64_t kv_heads, uint64_t head_dim, uint64_t first, uint64_t rows, void* scratch, uint64_t cap,
+                   unsigned int* over);
 bool residual_tq_fit(float* res, const uint16_t* q, const uint8_t* kc, const uint16_t* ks, const uint8_t* vc,
                      const uint16_t* vs, uint64_t q_heads, uint64_t kv_heads, uint64_t head_dim, uint64_t length,
                      uint64_t d, uint64_t rows, void* scratch, uint64_t cap);

@@ -479,6 +479,11 @@ __global__ void decode_plan_one(uint32_t* lens, uint32_t length, uint32_t nsplit
     }
 }
 
+// Row u of a causal chunk attends positions 0 .. first + u: its length, where decode_plan and decode_split read it.
+__global__ void causal_lens(uint32_t* lens, uint32_t first, uint32_t rows) {
+    for (uint32_t u = blockIdx.x * blockDim.x + threadIdx.x; u < rows; u += gridDim.x * blockDim.x) lens[u] = first + u + 1;
+}
+
 // decode_merge's arithmetic into the reference's residual instead of an answer: res[h] = {M, Σ e^(m_s - M)·l_s,
 // Σ e^(m_s - M)·acc_s} (kernels.cuh:1243-1255 over the splits), a workgroup per (query head, 64 dims), one row.
 template <int HD>
@@ -748,6 +753,73 @@ bool decode_one(uint16_t* o, float* res, const uint16_t* q, const uint16_t* k, c
             default: decode_merge_res<512><<<mgrid, 256, 0, st>>>(res, a.part, a.nsplit); break;
         }
     }
+    return true;
+}
+
+// Causal attention of `rows` rows over one contiguous cache as the split-K decode: row u attends positions 0 ..
+// first + u (every row's cache is the same, k_row 0) — the deferred causal chain's fused form where causal_mfma
+// takes no such shape (head_dim 512: latent attention's block prefill, where the latents are the keys and the
+// values). Its scratch is the chain's weights buffer, `cap` bytes. Answers false, launching nothing, when the shape
+// is not one decode_split takes or the scratch is too small.
+bool decode_causal(uint16_t* o, const uint16_t* q, const uint16_t* k, const uint16_t* v, uint64_t q_heads,
+                   uint64_t kv_heads, uint64_t head_dim, uint64_t first, uint64_t rows, void* scratch, uint64_t cap,
+                   unsigned int* over) {
+    const uint64_t most = first + rows;
+    if (!decode_shape_ok(q_heads, kv_heads, head_dim, most, rows) || (((uintptr_t)scratch) & 3u) != 0) return false;
+    const uint32_t hblocks = head_blocks(q_heads, kv_heads);
+    const uint64_t lens_at = part_at(rows, kv_heads * hblocks);
+    const uint64_t head = lens_at + (4 * rows + 255) / 256 * 256;
+    const uint64_t per_split = rows * q_heads * (head_dim + 2) * sizeof(float);
+    if (cap <= head || (cap - head) / per_split == 0) return false;
+    const uint64_t fit = (cap - head) / per_split;   // splits a row the scratch holds
+    const uint64_t step = (uint64_t)tile_keys((int)head_dim) * kWaves;
+    uint64_t chunk = choose_chunk(head_dim, kv_heads, hblocks, most, rows);
+    if ((most + chunk - 1) / chunk > fit) chunk = ((most + fit - 1) / fit + step - 1) / step * step;
+    DecodeArgs a;
+    a.chunk = (uint32_t)chunk;
+    a.nsplit = (uint32_t)((most + chunk - 1) / chunk);
+    if (a.nsplit > fit || a.nsplit > kMaxSplits) return false;
+    a.q = q; a.k = k; a.v = v; a.pages = nullptr; a.pages_row = 0; a.page_size = 0; a.k_row = 0;
+    a.q_heads = (uint32_t)q_heads; a.kv_heads = (uint32_t)kv_heads; a.group = (uint32_t)(q_heads / kv_heads);
+    a.hblocks = hblocks;
+    a.scale = 1.0f / sqrtf((float)head_dim);
+    a.counter = (uint32_t*)scratch;
+    uint32_t* lens = (uint32_t*)((char*)scratch + lens_at);
+    a.lens = lens;
+    a.plan = (const uint32_t*)((char*)scratch + kPlanAt);
+    a.done = (uint32_t*)((char*)scratch + done_at(rows));
+    a.part = (float*)((char*)scratch + head);
+    a.rows = (uint32_t)rows;
+    a.o = o;
+    a.over = over;
+    hipStream_t st = stream();
+    causal_lens<<<(uint32_t)((rows + 255) / 256), 256, 0, st>>>(lens, (uint32_t)first, (uint32_t)rows);
+    decode_plan<<<1, 256, 0, st>>>(lens, a.rows, a.chunk, (uint32_t*)a.plan, a.counter);
+    const dim3 grid((uint32_t)(rows * a.nsplit * kv_heads * hblocks));
+    prof_begin(kProfDecodeSplit);
+    if (head_dim == 512) {
+        if (k == v) decode_split<512, 2, false, false, true><<<grid, kThreads, 0, st>>>(a);
+        else decode_split<512, 2, false, false><<<grid, kThreads, 0, st>>>(a);
+    } else if (head_dim == 256) {
+        decode_split<256, kDefaultVariant, false, false><<<grid, kThreads, 0, st>>>(a);
+    } else if (head_dim == 128) {
+        decode_split<128, kDefaultVariant, false, false><<<grid, kThreads, 0, st>>>(a);
+    } else {
+        decode_split<64, kDefaultVariant, false, false><<<grid, kThreads, 0, st>>>(a);
+    }
+    prof_end(kProfDecodeSplit);
+    const dim3 mgrid((uint32_t)q_heads, (uint32_t)rows, (uint32_t)(head_dim / 64));
+    const bool wide = a.nsplit > 64;
+#define SILVANN_MERGE_C(HDV) \
+    if (wide) decode_merge<HDV, 16><<<mgrid, 1024, 0, st>>>(o, a.part, lens, a.q_heads, a.chunk, a.nsplit, over); \
+    else decode_merge<HDV, 4><<<mgrid, 256, 0, st>>>(o, a.part, lens, a.q_heads, a.chunk, a.nsplit, over);
+    switch (head_dim) {
+        case 64: SILVANN_MERGE_C(64) break;
+        case 128: SILVANN_MERGE_C(128) break;
+        case 256: SILVANN_MERGE_C(256) break;
+        default: SILVANN_MERGE_C(512) break;
+    }
+#undef SILVANN_MERGE_C
     return true;
 }
 

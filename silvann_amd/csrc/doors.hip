@@ -735,10 +735,19 @@ SILVANN_EXPORT void silvann_gfx950_attention_causal_mix(uint16_t* o, const float
     if (d.kind == kDeferCausalSoftmax && d.p == p && d.q_heads == q_heads && d.kv_heads == kv_heads &&
         d.head_dim == head_dim && d.first == first && d.rows == rows && d.st == stream()) {
         const Deferred r = d;
-        d = Deferred();   // the chain runs fused: p is never written
-        causal_paged_launch(o, nullptr, r.q, r.k, v, nullptr, 0, q_heads, kv_heads, head_dim, first, rows, over,
-                            "attention_causal_mix");
-        return;
+        if (causal_shape_ok(q_heads, kv_heads, head_dim, first, rows, false, 0)) {
+            d = Deferred();   // the chain runs fused on the matrix cores: p is never written
+            causal_paged_launch(o, nullptr, r.q, r.k, v, nullptr, 0, q_heads, kv_heads, head_dim, first, rows, over,
+                                "attention_causal_mix");
+            return;
+        }
+        // other shapes (head_dim 512): each row a decode over the same cache, p the scratch
+        const uint64_t cap = rows * q_heads * (first + rows) * sizeof(float);
+        if (decode_causal(o, r.q, r.k, v, q_heads, kv_heads, head_dim, first, rows, r.p, cap, over)) {
+            d = Deferred();
+            check_launch("attention_causal_mix");
+            return;
+        }
     }
     flush_deferred();
     if (!heads_ok("attention_causal_mix", q_heads, kv_heads, head_dim, rows)) return;
@@ -777,7 +786,8 @@ SILVANN_EXPORT void silvann_gfx950_attention_causal_scores_grouped(float* p, con
                                                                    uint64_t q_heads, uint64_t kv_heads,
                                                                    uint64_t head_dim, uint64_t first, uint64_t rows) {
     flush_deferred();
-    if (defer_enabled() && causal_shape_ok(q_heads, kv_heads, head_dim, first, rows, false, 0)) {
+    if (defer_enabled() && (causal_shape_ok(q_heads, kv_heads, head_dim, first, rows, false, 0) ||
+                            (decode_chain_shape(q_heads, kv_heads, head_dim, first + rows) && rows <= 65535))) {
         Deferred& d = deferred();
         d.kind = kDeferCausal; d.p = p; d.q = q; d.k = k;
         d.q_heads = q_heads; d.kv_heads = kv_heads; d.head_dim = head_dim; d.first = first; d.rows = rows;

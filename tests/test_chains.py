@@ -61,24 +61,31 @@ def test_weights_pair(oracle, qh, kvh, hd, length, interleave, fused):
         np.testing.assert_allclose(p, wp, rtol=1e-4, atol=1e-6)
 
 
-@pytest.mark.parametrize("qh,kvh,hd,first,rows,interleave,fused", [
-    (16, 2, 256, 77, 95, False, True),
-    (6, 3, 128, 10, 70, True, False),
-    (8, 1, 512, 5, 20, False, False),   # head_dim 512: no fused causal form, each door on its own
+@pytest.mark.parametrize("qh,kvh,hd,first,rows,interleave,route,shared", [
+    (16, 2, 256, 77, 95, False, "mfma", False),    # causal_mfma: the weights never written
+    (6, 3, 128, 10, 70, True, "doors", False),     # another door inside: each door on its own
+    (8, 1, 512, 600, 8, False, "decode", False),   # head_dim 512: each row a decode over the same cache
+    (64, 1, 512, 700, 4, False, "decode", True),   # latent attention's block prefill: the latents are k and v
+    (8, 1, 512, 5, 20, False, "doors", False),     # a prefix too short for the splits to fit: door by door
 ])
-def test_causal_chain(oracle, qh, kvh, hd, first, rows, interleave, fused):
+def test_causal_chain(oracle, qh, kvh, hd, first, rows, interleave, route, shared):
     q, k, v = _inputs(first + rows, qh, kvh, hd, first + rows, rows)
-    o, p, over, _ = emu.run_chain("causal", q, k, v, qh, kvh, hd, first, rows, interleave=interleave)
+    if shared:
+        v = k
+    o, p, over, _ = emu.run_chain("causal", q, k, None if shared else v, qh, kvh, hd, first, rows,
+                                  interleave=interleave)
     want, _ = oracle.causal_rows(q, k, v, None, 0, qh, kvh, hd, first, list(range(rows)))
     parity(o, want)
     assert over == 0
-    if fused:
+    wp = oracle.causal_softmax(oracle.causal_scores_grouped(q, k, qh, kvh, hd, first, rows), qh, first, rows)
+    # row r's weights are its first + r + 1 positions; past them the buffer keeps what it held
+    span = first + rows
+    valid = (np.arange(span)[None, :] <= first + np.repeat(np.arange(rows), qh)[:, None]).ravel()
+    if route == "mfma":
         assert np.all(p.view(np.uint32) == 0xFFFFFFFF)   # the weights were never written
+    elif route == "decode":
+        assert not np.allclose(p[valid], wp[valid], rtol=1e-4, atol=1e-6)   # the buffer held the splits' scratch
     else:
-        wp = oracle.causal_softmax(oracle.causal_scores_grouped(q, k, qh, kvh, hd, first, rows), qh, first, rows)
-        # row r's weights are its first + r + 1 positions; past them the buffer keeps what it held
-        span = first + rows
-        valid = (np.arange(span)[None, :] <= first + np.repeat(np.arange(rows), qh)[:, None]).ravel()
         np.testing.assert_allclose(p[valid], wp[valid], rtol=1e-4, atol=1e-6)
 
 

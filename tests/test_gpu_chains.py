@@ -136,3 +136,27 @@ def test_tier_verb_runs_fused(dev, oracle, d, length):
     np.testing.assert_allclose(g[:, 1:2] * at, o[:, 1:2], rtol=2e-3)
     parity(fin(g), fin(o))
     assert not doors.launch_failed()
+
+
+def test_latent_block_prefill_runs_fused(dev, oracle):
+    """GLM 5.3's block prefill chain (ai_z__glm_5_3/cpu/opcodes/layer__abi.cuh:1004-1009): causal_scores_grouped,
+    causal_softmax, causal_mix with one kv head, head_dim 512, the latent cache as both keys and values — each row a
+    split-K decode over the same cache, the weights buffer its scratch."""
+    heads, lat, first, rows = 64, 512, 5000, 64
+    print("case: latent block prefill chain", flush=True)
+    rng = np.random.default_rng(77)
+    q = rng.standard_normal(rows * heads * lat).astype(np.float16)
+    cache = rng.standard_normal((first + rows) * lat).astype(np.float16)
+    qd, cd = t(q, dev), t(cache, dev)
+    p = _z(dev, rows * heads * (first + rows))
+    o = _z(dev, rows * heads * lat, torch.float16)
+    over = _z(dev, 1, torch.int32)
+    doors.attention_causal_scores_grouped(p, qd, cd, heads, 1, lat, first, rows)
+    doors.attention_causal_softmax(p, heads, first, rows)
+    doors.attention_causal_mix(o, p, cd, heads, 1, lat, first, rows, over)
+    which = [0, 1, 31, rows - 1]
+    want, _ = oracle.causal_rows(q, cache, cache, None, 0, heads, 1, lat, first, which)
+    got = o.cpu().numpy().reshape(rows, heads * lat)[which].ravel()
+    parity(got, want)
+    assert int(over.item()) == 0
+    assert not doors.launch_failed()
