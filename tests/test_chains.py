@@ -30,7 +30,7 @@ def _inputs(seed, qh, kvh, hd, n, rows=1):
     (16, 2, 256, 2048, True, True, False),    # another door between: each door on its own
     (16, 2, 256, 2048, False, False, False),  # deferral off
     (8, 2, 128, 40, False, True, False),      # too short for the splits to fit: each door on its own
-    (64, 1, 512, 700, False, True, True),     # one kv head, head_dim 512
+    (32, 1, 512, 600, False, True, True),     # one kv head, head_dim 512, two head blocks
 ])
 def test_decode_pair(oracle, qh, kvh, hd, length, interleave, defer, fused):
     q, k, v = _inputs(qh + hd + length, qh, kvh, hd, length)
@@ -63,9 +63,9 @@ def test_weights_pair(oracle, qh, kvh, hd, length, interleave, fused):
 
 @pytest.mark.parametrize("qh,kvh,hd,first,rows,interleave,route,shared", [
     (16, 2, 256, 77, 95, False, "mfma", False),    # causal_mfma: the weights never written
-    (6, 3, 128, 10, 70, True, "doors", False),     # another door inside: each door on its own
-    (8, 1, 512, 600, 8, False, "decode", False),   # head_dim 512: each row a decode over the same cache
-    (64, 1, 512, 700, 4, False, "decode", True),   # latent attention's block prefill: the latents are k and v
+    (6, 3, 128, 10, 30, True, "doors", False),     # another door inside: each door on its own
+    (8, 1, 512, 530, 3, False, "decode", False),   # head_dim 512: each row a decode over the same cache
+    (20, 1, 512, 530, 2, False, "decode", True),   # latent attention's block prefill: the latents are k and v
     (8, 1, 512, 5, 20, False, "doors", False),     # a prefix too short for the splits to fit: door by door
 ])
 def test_causal_chain(oracle, qh, kvh, hd, first, rows, interleave, route, shared):
@@ -89,10 +89,10 @@ def test_causal_chain(oracle, qh, kvh, hd, first, rows, interleave, route, share
         np.testing.assert_allclose(p[valid], wp[valid], rtol=1e-4, atol=1e-6)
 
 
-@pytest.mark.parametrize("first,rows,interleave,fused", [(300, 40, False, True), (300, 40, True, False)])
+@pytest.mark.parametrize("first,rows,interleave,fused", [(100, 20, False, True), (100, 20, True, False)])
 def test_weights_rows_pair(oracle, first, rows, interleave, fused):
     """weights_rows + residual_mix_rows (the tiered prefill window's part 0) as the causal residual (row 140)."""
-    qh, kvh, hd = 16, 2, 256
+    qh, kvh, hd = 8, 2, 256
     q, k, v = _inputs(first + rows + 5, qh, kvh, hd, first + rows, rows)
     p, res, _, _ = emu.run_chain_residual("rows", q, k, None, v, None, qh, kvh, hd, first, rows=rows,
                                           interleave=interleave)

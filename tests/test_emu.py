@@ -79,7 +79,7 @@ def test_causal_residual_kernel(oracle, hd, qh, kvh, first, rows, ps):
 
 
 @pytest.mark.parametrize("qh,lens,ps,shared", [
-    (64, [300, 41], 0, True),       # latent attention's shape: 64 heads, one kv head, keys = values, 512 wide
+    (64, [130, 41], 0, True),       # latent attention's shape: 64 heads, one kv head, keys = values, 512 wide
     (20, [97], 64, True),           # two head blocks, the second part-full; paged
     (16, [130, 1], 0, False),       # head_dim 512 with values of their own
 ])
