@@ -93,6 +93,10 @@ void silvann_gfx950_attention_causal_scores_grouped(float* p, const uint16_t* q,
 /* gpu.cuh:192 attention_causal_softmax — kernels.cuh:1065-1081 */
 #define SILVANN_GFX950_ROW_ATTENTION_CAUSAL_SOFTMAX 98u
 void silvann_gfx950_attention_causal_softmax(float* p, uint64_t q_heads, uint64_t first, uint64_t rows);
+/* gpu.cuh:201 attention_softmax_sink — kernels.cuh:1115-1131: each of `rows` rows (`length` apart) its softmax with
+ * a sink, the sum taking one more term e^(sink[r]) (fp16) that weighs no position (DeepSeek V4's attention) */
+#define SILVANN_GFX950_ROW_ATTENTION_SOFTMAX_SINK 107u
+void silvann_gfx950_attention_softmax_sink(float* p, const uint16_t* sink, uint64_t rows, uint64_t length);
 /* gpu.cuh:195 attention_weights_rows — doors.cuh:201-204,417-424 (attention_weights a row at a time) */
 #define SILVANN_GFX950_ROW_ATTENTION_WEIGHTS_ROWS 101u
 void silvann_gfx950_attention_weights_rows(float* p, float* res, const uint16_t* q, const uint16_t* k,

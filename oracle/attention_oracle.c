@@ -522,6 +522,24 @@ void oracle_attention_causal_rows(uint16_t* o, const uint16_t* q, const uint16_t
     free(p); free(kg); free(vg);
 }
 
+/* kernels.cuh:1115-1131 — each of `rows` rows of `length` weights (row r at p + r·length) its softmax with a sink:
+ * the top over sink[r] and the row, e^(x - top), normalised by their sum plus e^(sink[r] - top). */
+void oracle_attention_softmax_sink(float* p, const uint16_t* sink, uint64_t rows, uint64_t length) {
+    for (uint64_t r = 0; r < rows; ++r) {
+        float* ph = p + r * length;
+        const float sk = h2f(sink[r]);
+        float top = sk;
+        for (uint64_t t = 0; t < length; ++t) if (ph[t] > top) top = ph[t];
+        float part = 0.0f;
+        for (uint64_t t = 0; t < length; ++t) {
+            ph[t] = expf(ph[t] - top);
+            part += ph[t];
+        }
+        const float inv = 1.0f / (part + expf(sk - top));
+        for (uint64_t t = 0; t < length; ++t) ph[t] *= inv;
+    }
+}
+
 /* kernels.cuh:1710-1726 (`rope_rows`) — each row's heads turned by that row's angles: row r's at cs + r·rot, the rot/2
  * cosines then the rot/2 sines; of every head (head_stride apart; rows row_stride apart) elements k and k + rot/2,
  * for k < rot/2, become a·c − b·s and b·c + a·s, rounded to fp16 (overflow to *over). o may be x.

@@ -31,6 +31,7 @@ SIGNATURES = {
     "silvann_gfx950_attention_softmax_rows": [_p, _u64, _u64],
     "silvann_gfx950_attention_causal_scores_grouped": [_p, _p, _p, _u64, _u64, _u64, _u64, _u64],
     "silvann_gfx950_attention_causal_softmax": [_p, _u64, _u64, _u64],
+    "silvann_gfx950_attention_softmax_sink": [_p, _p, _u64, _u64],
     "silvann_gfx950_attention_weights_rows": [_p, _p, _p, _p, _u64, _u64, _u64, _u64, _u64],
     "silvann_gfx950_attention_residual_mix_rows": [_p, _p, _p, _u64, _u64, _u64, _u64, _u64],
     "silvann_gfx950_attention_weights_tq_rows": [_p, _p, _p, _p, _p, _u64, _u64, _u64, _u64, _u64, _u64],

@@ -399,10 +399,12 @@ void decode_split(DecodeArgs a) {
 // at a time with eight independent sums (their loads in flight together); a lane holds one dim; the waves'
 // sums meet in LDS. Every split's weight e^(m_s - M) needs the head's largest m first, folded over the
 // whole workgroup.
-template <int HD, int kMergeWaves>
+// SINK: each head's sum takes one more term, e^(sink[h] - M) with M over the sink too (attention_softmax_sink's
+// weights, kernels.cuh:1115-1131, mixed: one query row).
+template <int HD, int kMergeWaves, bool SINK = false>
 __global__ __launch_bounds__(64 * kMergeWaves) void decode_merge(uint16_t* o, const float* part, const uint32_t* lens,
                                                                  uint32_t q_heads, uint32_t chunk, uint32_t nsplit,
-                                                                 unsigned int* over) {
+                                                                 unsigned int* over, const uint16_t* sink) {
     __shared__ float red[kMergeWaves];
     __shared__ float accs[kMergeWaves][64];
     __shared__ float ls[kMergeWaves];
@@ -426,6 +428,11 @@ __global__ __launch_bounds__(64 * kMergeWaves) void decode_merge(uint16_t* o, co
     float M = red[0];
 #pragma unroll
     for (int k = 1; k < kMergeWaves; ++k) M = fmaxf(M, red[k]);
+    float sk = 0.0f;
+    if constexpr (SINK) {
+        sk = half_bits_to_float(sink[h]);
+        M = fmaxf(M, sk);
+    }
 
     constexpr int U = 8;
     float accu[U], lsu[U];
@@ -463,6 +470,7 @@ __global__ __launch_bounds__(64 * kMergeWaves) void decode_merge(uint16_t* o, co
         L += ls[k];
         A += accs[k][lane];
     }
+    if constexpr (SINK) L += fast_exp(sk - M);
     bool hit = false;
     out[d] = to_half(A / L, hit);
     if (hit) *over = kFaultOverflow;
@@ -672,8 +680,8 @@ void decode_paged_launch(uint16_t* o, const uint16_t* q, const uint16_t* k, cons
     prof_begin(kProfDecodeMerge);
     const bool wide = a.nsplit > 64;
 #define SILVANN_MERGE(HDV) \
-    if (wide) decode_merge<HDV, 16><<<mgrid, 1024, 0, st>>>(o, a.part, lens, a.q_heads, a.chunk, a.nsplit, over); \
-    else decode_merge<HDV, 4><<<mgrid, 256, 0, st>>>(o, a.part, lens, a.q_heads, a.chunk, a.nsplit, over);
+    if (wide) decode_merge<HDV, 16><<<mgrid, 1024, 0, st>>>(o, a.part, lens, a.q_heads, a.chunk, a.nsplit, over, nullptr); \
+    else decode_merge<HDV, 4><<<mgrid, 256, 0, st>>>(o, a.part, lens, a.q_heads, a.chunk, a.nsplit, over, nullptr);
     switch (head_dim) {
         case 64: SILVANN_MERGE(64) break;
         case 128: SILVANN_MERGE(128) break;
@@ -690,7 +698,9 @@ void decode_paged_launch(uint16_t* o, const uint16_t* q, const uint16_t* k, cons
 // bytes, which the fused form never fills with weights: the splits are made long enough for their residuals to fit
 // it. Answers false, launching nothing, when the shape is not one decode_split takes or no split length fits.
 bool decode_one(uint16_t* o, float* res, const uint16_t* q, const uint16_t* k, const uint16_t* v, uint64_t q_heads,
-                uint64_t kv_heads, uint64_t head_dim, uint64_t length, void* scratch, uint64_t cap, unsigned int* over) {
+                uint64_t kv_heads, uint64_t head_dim, uint64_t length, void* scratch, uint64_t cap, unsigned int* over,
+                const uint16_t* sink) {
+    if (sink && !o) return false;   // a sink weighs the answer's sum; the residual form has none
     if (!decode_shape_ok(q_heads, kv_heads, head_dim, length, 1) || (((uintptr_t)scratch) & 3u) != 0) return false;
     const uint32_t hblocks = head_blocks(q_heads, kv_heads);
     const uint64_t head = part_at(1, kv_heads * hblocks), per_split = q_heads * (head_dim + 2) * sizeof(float);
@@ -736,8 +746,11 @@ bool decode_one(uint16_t* o, float* res, const uint16_t* q, const uint16_t* k, c
     if (o) {
         const bool wide = nsplit > 64;
 #define SILVANN_MERGE_ONE(HDV) \
-        if (wide) decode_merge<HDV, 16><<<mgrid, 1024, 0, st>>>(o, a.part, lens, a.q_heads, a.chunk, a.nsplit, over); \
-        else decode_merge<HDV, 4><<<mgrid, 256, 0, st>>>(o, a.part, lens, a.q_heads, a.chunk, a.nsplit, over);
+        if (sink) { \
+            if (wide) decode_merge<HDV, 16, true><<<mgrid, 1024, 0, st>>>(o, a.part, lens, a.q_heads, a.chunk, a.nsplit, over, sink); \
+            else decode_merge<HDV, 4, true><<<mgrid, 256, 0, st>>>(o, a.part, lens, a.q_heads, a.chunk, a.nsplit, over, sink); \
+        } else if (wide) decode_merge<HDV, 16><<<mgrid, 1024, 0, st>>>(o, a.part, lens, a.q_heads, a.chunk, a.nsplit, over, nullptr); \
+        else decode_merge<HDV, 4><<<mgrid, 256, 0, st>>>(o, a.part, lens, a.q_heads, a.chunk, a.nsplit, over, nullptr);
         switch (head_dim) {
             case 64: SILVANN_MERGE_ONE(64) break;
             case 128: SILVANN_MERGE_ONE(128) break;
@@ -811,8 +824,8 @@ bool decode_causal(uint16_t* o, const uint16_t* q, const uint16_t* k, const uint
     const dim3 mgrid((uint32_t)q_heads, (uint32_t)rows, (uint32_t)(head_dim / 64));
     const bool wide = a.nsplit > 64;
 #define SILVANN_MERGE_C(HDV) \
-    if (wide) decode_merge<HDV, 16><<<mgrid, 1024, 0, st>>>(o, a.part, lens, a.q_heads, a.chunk, a.nsplit, over); \
-    else decode_merge<HDV, 4><<<mgrid, 256, 0, st>>>(o, a.part, lens, a.q_heads, a.chunk, a.nsplit, over);
+    if (wide) decode_merge<HDV, 16><<<mgrid, 1024, 0, st>>>(o, a.part, lens, a.q_heads, a.chunk, a.nsplit, over, nullptr); \
+    else decode_merge<HDV, 4><<<mgrid, 256, 0, st>>>(o, a.part, lens, a.q_heads, a.chunk, a.nsplit, over, nullptr);
     switch (head_dim) {
         case 64: SILVANN_MERGE_C(64) break;
         case 128: SILVANN_MERGE_C(128) break;

@@ -169,6 +169,35 @@ __global__ __launch_bounds__(256) void softmax_rows(float* p, float* res, Geom G
     for (uint64_t t = threadIdx.x; t < len; t += 256) ph[t] *= inv;
 }
 
+// Row r's softmax with a sink (kernels.cuh:1115-1131): the top over sink[r] and the row, e^(x - top), normalised by
+// their sum plus e^(sink[r] - top) — weight a row may give to none of its positions. A workgroup a row.
+__global__ __launch_bounds__(256) void softmax_sink_rows(float* p, const uint16_t* sink, uint64_t rows,
+                                                         uint64_t length) {
+    __shared__ float red[8];
+    const uint64_t r = blockIdx.x + (uint64_t)blockIdx.y * gridDim.x;
+    if (r >= rows) return;
+    float* ph = p + r * length;
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    const float sk = half_bits_to_float(sink[r]);
+    float mx = sk;
+    for (uint64_t t = threadIdx.x; t < length; t += 256) mx = fmaxf(mx, ph[t]);
+    mx = wave_max(mx);
+    if (lane == 0) red[w] = mx;
+    __syncthreads();
+    const float top = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    float part = 0.0f;
+    for (uint64_t t = threadIdx.x; t < length; t += 256) {
+        const float e = expf(ph[t] - top);
+        ph[t] = e;
+        part += e;
+    }
+    part = wave_sum(part);
+    if (lane == 0) red[4 + w] = part;
+    __syncthreads();
+    const float inv = 1.0f / (red[4] + red[5] + red[6] + red[7] + expf(sk - top));
+    for (uint64_t t = threadIdx.x; t < length; t += 256) ph[t] *= inv;
+}
+
 // o[h][d] = Σ_t p[h][t] v_t[d] for a block of query heads of one kv head and 64 dims; into fp16 `o` (with
 // the overflow flag) or, `acc_out` set, into the fp32 residual's acc.
 template <int MODE>
@@ -581,6 +610,30 @@ void weights_tq_rows_body(float* p, float* res, const uint16_t* q, const uint8_t
     check_launch("attention_weights_tq_rows");
 }
 
+void scores_grouped_body(float* p, const uint16_t* q, const uint16_t* k, uint64_t q_heads, uint64_t kv_heads,
+                         uint64_t head_dim, uint64_t length) {
+    if (!heads_ok("attention_scores_grouped", q_heads, kv_heads, head_dim, 1)) return;
+    Geom G = geom(kSingle, q_heads, kv_heads, head_dim);
+    G.length = length;
+    launch_scores(p, q, k, G, 1, length);
+    check_launch("attention_scores_grouped");
+}
+
+void softmax_rows_body(float* p, uint64_t rows, uint64_t length) {
+    Geom G = geom(kSingle, 1, 1, 1);   // row r at r·length, `length` long: the one-query geometry
+    G.length = length;
+    if (length == 0) return;
+    launch_softmax(p, nullptr, G, rows);
+    check_launch("attention_softmax_rows");
+}
+
+void softmax_sink_body(float* p, const uint16_t* sink, uint64_t rows, uint64_t length) {
+    if (rows == 0) return;
+    const dim3 grid((uint32_t)(rows < 65535 ? rows : 65535), (uint32_t)((rows + 65534) / 65535));
+    softmax_sink_rows<<<grid, 256, 0, stream()>>>(p, sink, rows, length);
+    check_launch("attention_softmax_sink");
+}
+
 // A door records its chain's first step only when a fused form could take the chain (and the shape is valid:
 // an invalid one runs at once, to be refused).
 bool decode_chain_shape(uint64_t q_heads, uint64_t kv_heads, uint64_t head_dim, uint64_t length) {
@@ -610,6 +663,15 @@ void flush_deferred() {
             break;
         case kDeferWeightsTq:
             weights_tq_body(r.p, r.res, r.q, r.codes, r.scales, r.q_heads, r.kv_heads, r.head_dim, r.length, r.d);
+            break;
+        case kDeferGrouped: scores_grouped_body(r.p, r.q, r.k, r.q_heads, r.kv_heads, r.head_dim, r.length); break;
+        case kDeferGroupedSoftmax:
+            scores_grouped_body(r.p, r.q, r.k, r.q_heads, r.kv_heads, r.head_dim, r.length);
+            softmax_rows_body(r.p, r.q_heads, r.length);
+            break;
+        case kDeferGroupedSink:
+            scores_grouped_body(r.p, r.q, r.k, r.q_heads, r.kv_heads, r.head_dim, r.length);
+            softmax_sink_body(r.p, r.sink, r.q_heads, r.length);
             break;
         case kDeferWeightsTqRows:
             weights_tq_rows_body(r.p, r.res, r.q, r.codes, r.scales, r.q_heads, r.kv_heads, r.head_dim, r.length, r.d,
@@ -642,10 +704,11 @@ SILVANN_EXPORT void silvann_gfx950_attention_mix(uint16_t* o, const float* p, co
                                                  uint64_t kv_heads, uint64_t head_dim, uint64_t length,
                                                  unsigned int* over) {
     Deferred& d = deferred();
-    if (d.kind == kDeferScores && d.p == p && d.q_heads == q_heads && d.kv_heads == kv_heads &&
-        d.head_dim == head_dim && d.length == length && d.st == stream() &&
+    const bool chain = d.kind == kDeferScores || d.kind == kDeferGroupedSoftmax || d.kind == kDeferGroupedSink;
+    if (chain && d.p == p && d.q_heads == q_heads && d.kv_heads == kv_heads && d.head_dim == head_dim &&
+        d.length == length && d.st == stream() &&
         decode_one(o, nullptr, d.q, d.k, v, q_heads, kv_heads, head_dim, length, (void*)p,
-                   q_heads * length * sizeof(float), over)) {
+                   q_heads * length * sizeof(float), over, d.kind == kDeferGroupedSink ? d.sink : nullptr)) {
         d = Deferred();   // the chain ran fused: p holds the splits' residuals, not weights
         check_launch("attention_mix");
         return;
@@ -762,22 +825,38 @@ SILVANN_EXPORT void silvann_gfx950_attention_causal_mix(uint16_t* o, const float
 SILVANN_EXPORT void silvann_gfx950_attention_scores_grouped(float* p, const uint16_t* q, const uint16_t* k,
                                                             uint64_t q_heads, uint64_t kv_heads, uint64_t head_dim,
                                                             uint64_t length) {
-    silvann::flush_deferred();
-    if (!heads_ok("attention_scores_grouped", q_heads, kv_heads, head_dim, 1)) return;
-    Geom G = geom(kSingle, q_heads, kv_heads, head_dim);
-    G.length = length;
-    launch_scores(p, q, k, G, 1, length);
-    check_launch("attention_scores_grouped");
+    flush_deferred();
+    if (defer_enabled() && decode_chain_shape(q_heads, kv_heads, head_dim, length)) {
+        Deferred& d = deferred();   // with softmax_rows or softmax_sink, then mix: the split-K decode
+        d.kind = kDeferGrouped; d.p = p; d.q = q; d.k = k;
+        d.q_heads = q_heads; d.kv_heads = kv_heads; d.head_dim = head_dim; d.length = length; d.st = stream();
+        return;
+    }
+    scores_grouped_body(p, q, k, q_heads, kv_heads, head_dim, length);
 }
 
 // gpu.cuh:190 — kernels.cuh:1095-1097
 SILVANN_EXPORT void silvann_gfx950_attention_softmax_rows(float* p, uint64_t rows, uint64_t length) {
-    silvann::flush_deferred();
-    Geom G = geom(kSingle, 1, 1, 1);   // row r at r·length, `length` long: the one-query geometry
-    G.length = length;
-    if (length == 0) return;
-    launch_softmax(p, nullptr, G, rows);
-    check_launch("attention_softmax_rows");
+    Deferred& d = deferred();
+    if (d.kind == kDeferGrouped && d.p == p && d.q_heads == rows && d.length == length && d.st == stream()) {
+        d.kind = kDeferGroupedSoftmax;   // the chain's second step, recorded too
+        return;
+    }
+    flush_deferred();
+    softmax_rows_body(p, rows, length);
+}
+
+// gpu.cuh:201 — kernels.cuh:1115-1131
+SILVANN_EXPORT void silvann_gfx950_attention_softmax_sink(float* p, const uint16_t* sink, uint64_t rows,
+                                                          uint64_t length) {
+    Deferred& d = deferred();
+    if (d.kind == kDeferGrouped && d.p == p && d.q_heads == rows && d.length == length && d.st == stream()) {
+        d.kind = kDeferGroupedSink;   // the chain's second step, recorded with its sink
+        d.sink = sink;
+        return;
+    }
+    flush_deferred();
+    softmax_sink_body(p, sink, rows, length);
 }
 
 // gpu.cuh:191 — kernels.cuh:1028-1061

@@ -162,6 +162,7 @@ SILVANN_EXPORT uint32_t silvann_gfx950_attention_install(void* nn_doors) {
         {SILVANN_GFX950_ROW_ATTENTION_SOFTMAX_ROWS, (void*)&silvann_gfx950_attention_softmax_rows},
         {SILVANN_GFX950_ROW_ATTENTION_CAUSAL_SCORES_GROUPED, (void*)&silvann_gfx950_attention_causal_scores_grouped},
         {SILVANN_GFX950_ROW_ATTENTION_CAUSAL_SOFTMAX, (void*)&silvann_gfx950_attention_causal_softmax},
+        {SILVANN_GFX950_ROW_ATTENTION_SOFTMAX_SINK, (void*)&silvann_gfx950_attention_softmax_sink},
         {SILVANN_GFX950_ROW_ATTENTION_WEIGHTS_ROWS, (void*)&silvann_gfx950_attention_weights_rows},
         {SILVANN_GFX950_ROW_ATTENTION_RESIDUAL_MIX_ROWS, (void*)&silvann_gfx950_attention_residual_mix_rows},
         {SILVANN_GFX950_ROW_ATTENTION_WEIGHTS_TQ_ROWS, (void*)&silvann_gfx950_attention_weights_tq_rows},
@@ -190,5 +191,5 @@ SILVANN_EXPORT uint32_t silvann_gfx950_attention_install(void* nn_doors) {
 }
 
 SILVANN_EXPORT const char* silvann_gfx950_version(void) {
-    return "gfx950 decode-splitk-mfma16 causal-mfma32 tq-mfma16 cache-writer doors-27 v1";
+    return "gfx950 decode-splitk-mfma16 causal-mfma32 tq-mfma16 cache-writer doors-28 deferred-chains v1";
 }

@@ -43,6 +43,7 @@ attention_scores_grouped = _door("attention_scores_grouped")
 attention_softmax_rows = _door("attention_softmax_rows")
 attention_causal_scores_grouped = _door("attention_causal_scores_grouped")
 attention_causal_softmax = _door("attention_causal_softmax")
+attention_softmax_sink = _door("attention_softmax_sink")
 attention_weights_rows = _door("attention_weights_rows")
 attention_residual_mix_rows = _door("attention_residual_mix_rows")
 attention_weights_tq_rows = _door("attention_weights_tq_rows")

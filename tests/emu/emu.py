@@ -140,14 +140,16 @@ def run_fp16(q, k, v, qh, kvh, hd, length=0, first=0, rows=0, timeout: int = 900
 
 def run_grouped(q, k, v, qh, kvh, hd, most, lens=None, k_row=0, timeout: int = 900):
     """attention_scores_grouped + attention_softmax_rows + attention_mix over `most` keys (lens None), or
-    scores_grouped_rows + softmax_lens + mix_rows for one row a lens entry: raw scores, weights and answers."""
+    scores_grouped_rows + softmax_lens + mix_rows for one row a lens entry, each door on its own: raw scores,
+    weights and answers."""
     many = lens is not None
     rows = len(lens) if many else 1
     params = f"{'grouped_rows' if many else 'grouped'} {qh} {kvh} {hd} {most} {rows} 0 0 {k_row}"
     files = {"q": q, "k": k, "v": v}
     if many:
         files["lens"] = np.ascontiguousarray(lens, np.uint32)
-    return _run(files, params, None, timeout, outs=(("p", np.float32), ("p_soft", np.float32), ("o", np.uint16)))
+    return _run(files, params, {"SILVANN_GFX950_DEFER": "0"}, timeout,
+                outs=(("p", np.float32), ("p_soft", np.float32), ("o", np.uint16)))
 
 
 def run_rope_rows(x, cs, rows, heads, head_stride, row_stride, rot, timeout: int = 900):
@@ -182,3 +184,14 @@ def run_chain_residual(kind, q, kcodes, kscales, vcodes, vscales, qh, kvh, hd, a
              f"{1 if interleave else 0} 0"
     files = {"q": q, "k": kcodes, "v": vcodes, "pages": kscales, "lens": vscales}
     return _run(files, params, env, timeout, outs=(("p", np.float32), ("res", np.float32)))
+
+
+def run_chain_grouped(q, k, v, qh, kvh, hd, length, sink=None, interleave=False, timeout: int = 900):
+    """Latent attention's chain as GLM and DeepSeek call it: attention_scores_grouped, then attention_softmax_rows
+    (sink None) or attention_softmax_sink, then attention_mix. `v` None: the keys are the values. The answers, the
+    weights buffer afterwards and the fault word."""
+    params = f"chain_grp {qh} {kvh} {hd} {length} {0 if sink is None else 1} {1 if interleave else 0} 0 0"
+    files = {"q": q, "k": k, "v": v}
+    if sink is not None:
+        files["lens"] = np.ascontiguousarray(sink, np.uint16)
+    return _run(files, params, None, timeout, outs=(("o", np.float16), ("p", np.float32)))

@@ -229,6 +229,27 @@ int main(int argc, char** argv) {
         save(d + "/over.bin", over, 4);
         fprintf(stderr, "emu done: refused %d, wave exchanges %ld\n", silvann::emu_refused, (long)emu::ops);
         return silvann::emu_refused ? 5 : 0;
+    } else if (std::string(mode) == "chain_grp") {
+        // scores_grouped, softmax_rows (a1 = 0) or softmax_sink (a1 = 1, the sink in lens.bin), mix over a0 keys;
+        // ps = 1 puts another door between the softmax and the mix
+        const unsigned long length = a0;
+        float* p = (float*)guarded(qh * length * 4, "p");
+        memset(p, 0xFF, qh * length * 4);
+        char* sink = a1 ? load(d + "/lens.bin", "sink") : nullptr;
+        const unsigned long on = qh * hd * 2;
+        uint16_t* o16 = (uint16_t*)guarded(on, "o");
+        memset(o16, 0xFF, on);
+        silvann_gfx950_attention_scores_grouped(p, (const uint16_t*)q, (const uint16_t*)k, qh, kvh, hd, length);
+        if (a1) silvann_gfx950_attention_softmax_sink(p, (const uint16_t*)sink, qh, length);
+        else silvann_gfx950_attention_softmax_rows(p, qh, length);
+        if (ps == 1) silvann_gfx950_attention_finish(nullptr, nullptr, 0, hd, over);
+        silvann_gfx950_attention_mix(o16, p, (const uint16_t*)v, qh, kvh, hd, length, over);
+        silvann_gfx950_flush();
+        save(d + "/o.bin", o16, on);
+        save(d + "/p.bin", p, qh * length * 4);
+        save(d + "/over.bin", over, 4);
+        fprintf(stderr, "emu done: refused %d, wave exchanges %ld\n", silvann::emu_refused, (long)emu::ops);
+        return silvann::emu_refused ? 5 : 0;
     } else if (std::string(mode) == "chain_causal") {
         // causal_scores_grouped, causal_softmax, causal_mix from a0 = first over a1 = rows, as nn__attention__rows
         // calls them; ps = 1 puts another door (a finish of nothing) between the softmax and the mix

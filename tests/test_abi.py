@@ -90,7 +90,7 @@ def test_install_writes_the_rows_a_table_reaches():
                 assert buf[1 + i] == _fn_addr(L, "silvann_gfx950_" + rows[i].lower()), rows[i]
             else:
                 assert buf[1 + i] == sentinel + i, i
-    assert len([i for i in rows if i < NN_ROWS]) == len(ROWS) == 22
+    assert len([i for i in rows if i < NN_ROWS]) == len(ROWS) == 23
     assert L.silvann_gfx950_attention_install(None) == 0
 
 

@@ -130,3 +130,26 @@ def test_tq_pair(oracle, kind, d, hd, length, rows, interleave, fused):
     np.testing.assert_allclose(g[:, 2:] * at, o[:, 2:], rtol=0, atol=4e-3 * float(np.abs(o[:, 2:]).max()))
     if not fused:   # each door on its own: the oracle's residual to the doors' own bar
         np.testing.assert_allclose(res, wres, rtol=1e-4, atol=1e-5 * float(np.abs(wres).max()))
+
+
+@pytest.mark.parametrize("qh,hd,length,sink,interleave,fused", [
+    (16, 512, 1100, False, False, True),   # GLM 5.3: scores_grouped, softmax_rows, mix over the latents
+    (16, 512, 1100, True, False, True),    # DeepSeek V4: the softmax with a sink
+    (16, 512, 1100, True, True, False),    # another door inside: each door on its own
+])
+def test_grouped_chain(oracle, qh, hd, length, sink, interleave, fused):
+    """Latent attention's chain (one kv head, the latents as keys and values) through the library's doors."""
+    rng = np.random.default_rng(qh + length + sink)
+    q = rng.standard_normal(qh * hd).astype(np.float16)
+    lat = rng.standard_normal(length * hd).astype(np.float16)
+    s = (rng.standard_normal(qh) * 2 + 1).astype(np.float16).view(np.uint16) if sink else None
+    o, p, over, _ = emu.run_chain_grouped(q, lat, None, qh, 1, hd, length, sink=s, interleave=interleave)
+    raw = oracle.scores_grouped(q, lat, qh, 1, hd, length)
+    wp = oracle.softmax_sink(raw, s, qh, length) if sink else oracle.softmax_rows(raw, qh, length)
+    want, _ = oracle.mix(wp, lat, qh, 1, hd, length)
+    parity(o, want)
+    assert over == 0
+    if fused:
+        assert not np.allclose(p, wp, rtol=1e-4, atol=1e-6)
+    else:
+        np.testing.assert_allclose(p, wp, rtol=1e-4, atol=1e-6)

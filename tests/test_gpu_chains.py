@@ -160,3 +160,33 @@ def test_latent_block_prefill_runs_fused(dev, oracle):
     parity(got, want)
     assert int(over.item()) == 0
     assert not doors.launch_failed()
+
+
+@pytest.mark.parametrize("heads,length,sink", [(64, 2048, False), (64, 2048, True), (16, 100000, True)])
+def test_latent_decode_chain_runs_fused(dev, oracle, heads, length, sink):
+    """Latent attention's decode chain: GLM 5.3's scores_grouped, softmax_rows, mix (layer__abi.cuh:283-289) and
+    DeepSeek V4's with softmax_sink (ai_deepseek_4/cpu/opcodes/layer__abi.cuh:299-301), one kv head, 512-wide
+    latents as keys and values — as one split-K decode, the sink folded into its merge."""
+    hd = 512
+    print(f"case: latent decode chain heads{heads} length{length} sink{sink}", flush=True)
+    rng = np.random.default_rng(heads + length + sink)
+    q = rng.standard_normal(heads * hd).astype(np.float16)
+    lat = rng.standard_normal(length * hd).astype(np.float16)
+    s = (rng.standard_normal(heads) * 2 + 1).astype(np.float16).view(np.uint16)
+    qd, ld = t(q, dev), t(lat, dev)
+    p = _z(dev, heads * length)
+    o = _z(dev, heads * hd, torch.float16)
+    over = _z(dev, 1, torch.int32)
+    doors.attention_scores_grouped(p, qd, ld, heads, 1, hd, length)
+    if sink:
+        doors.attention_softmax_sink(p, t(s, dev), heads, length)
+    else:
+        doors.attention_softmax_rows(p, heads, length)
+    doors.attention_mix(o, p, ld, heads, 1, hd, length, over)
+    raw = oracle.scores_grouped(q, lat, heads, 1, hd, length)
+    wp = oracle.softmax_sink(raw, s, heads, length) if sink else oracle.softmax_rows(raw, heads, length)
+    want, _ = oracle.mix(wp, lat, heads, 1, hd, length)
+    parity(o.cpu().numpy(), want)
+    assert int(over.item()) == 0
+    assert not np.allclose(p.cpu().numpy(), wp, rtol=1e-4, atol=1e-6)   # fused: no weights were written
+    assert not doors.launch_failed()

@@ -242,3 +242,4 @@ def test_rows_attention_passes(dev, oracle):
     verbs.rows_attention(t(q, dev), t(k, dev), t(v, dev), scores, att, qh, kvh, hd, first, rows, over)
     wo, _ = oracle.causal_rows(q, k, v, None, 0, qh, kvh, hd, first, list(range(rows)))
     parity(att.cpu().numpy(), wo)
+

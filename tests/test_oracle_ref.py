@@ -90,3 +90,29 @@ def test_lens_rows(oracle, ref):
     a = oracle.mix_rows(o_row, p, p_row, v, k_row, lens, qh, kvh, hd, rows)[0].view(np.uint16).astype(np.int32)
     b = ref.mix_rows(o_row, p, p_row, v, k_row, lens, qh, kvh, hd, rows)[0].view(np.uint16).astype(np.int32)
     assert np.max(np.abs(a - b)) <= 1          # same sign everywhere here, so bits 1 apart = 1 ulp
+
+
+@pytest.mark.parametrize("rows,length,sink_at", [(16, 700, 0.0), (5, 33, 9.0), (3, 1, -40.0)])
+def test_softmax_sink(oracle, ref, rows, length, sink_at):
+    """attention_softmax_sink (gpu.cuh:201): the oracle is the family's door to the bit, with sinks below, inside and
+    above the scores' range (a large sink takes the top, kernels.cuh:1112-1114)."""
+    rng = np.random.default_rng(rows + length)
+    p = (rng.standard_normal(rows * length) * 3).astype(np.float32)
+    sink = (sink_at + rng.standard_normal(rows)).astype(np.float16).view(np.uint16)
+    same(oracle.softmax_sink(p, sink, rows, length), ref.softmax_sink(p, sink, rows, length))
+
+
+def test_softmax_sink_without_a_sink_is_the_softmax(oracle):
+    """A sink of -inf weighs nothing: the row softmax (kernels.cuh:1085-1094) to fp32 rounding."""
+    rng = np.random.default_rng(3)
+    rows, length = 4, 300
+    p = rng.standard_normal(rows * length).astype(np.float32)
+    sink = np.full(rows, np.float16(-np.inf)).view(np.uint16)
+    np.testing.assert_allclose(oracle.softmax_sink(p, sink, rows, length), oracle.softmax_rows(p, rows, length),
+                               rtol=1e-6, atol=1e-9)
+    # and the sink's own weight is what the row gives up: 1 - Σ p = e^(s - top) / (Σ e^(x - top) + e^(s - top))
+    sink = np.full(rows, np.float16(1.5)).view(np.uint16)
+    got = oracle.softmax_sink(p, sink, rows, length).reshape(rows, length).astype(np.float64)
+    x = p.reshape(rows, length).astype(np.float64)
+    want = 1.0 - np.exp(1.5) / (np.exp(x).sum(axis=1) + np.exp(1.5))
+    np.testing.assert_allclose(got.sum(axis=1), want, rtol=1e-5)
