@@ -333,6 +333,39 @@ def cpu_baseline(w, threads):
                       f"{total:.1f} s of CPU work; pages gathered to contiguous outside the timing"}
 
 
+def cpu_baseline_prefill(w, threads, budget=10.0):
+    """The reference x86_avx2 family's prefill doors beside the causal line: the last rows of the chunk (the heaviest,
+    each over the whole prefix) through attention_causal_scores_grouped, attention_causal_softmax and
+    attention_causal_mix, as the rows verb calls them (attention__abi.cuh:407-414), over the gathered contiguous cache,
+    repeated for about `budget` seconds. TFLOP/s of unmasked (query, key) pairs, 4·q_heads·head_dim each."""
+    import numpy as np
+    from oracle.oracle import RefFamily, ref_available
+    if not ref_available():
+        return None
+    host = lambda a: a.cpu().numpy() if hasattr(a, "cpu") else a  # noqa: E731
+    qh, kvh, hd = w.q_heads, w.kv_heads, w.head_dim
+    sample = 16
+    first = w.first + w.rows - sample
+    hw = type(w)(**{**w.__dict__, "q": host(w.q), "k": host(w.k), "v": host(w.v)})
+    k, v = hw.gathered()
+    q = hw.q[(w.rows - sample) * qh * hd:]
+    os.environ["SILVANN_CPU_THREADS"] = str(max(threads - 1, 0))
+    R = RefFamily()
+    flops = 4 * qh * hd * sum(first + i + 1 for i in range(sample))
+    reps, total = 0, 0.0
+    while total < budget and reps < 100:
+        t0 = time.perf_counter()
+        p = R.causal_scores_grouped(q, k, qh, kvh, hd, first, sample)
+        p = R.causal_softmax(p, qh, first, sample)
+        R.causal_mix(p, v, qh, kvh, hd, first, sample)
+        total += time.perf_counter() - t0
+        reps += 1
+    return {"value": flops * reps / total / 1e12, "unit": "TFLOP/s", "cores": threads, "kind": "reference",
+            "sample": f"the chunk's last {sample} rows (positions {first}..{first + sample - 1}, each over its whole "
+                      f"prefix) x{reps}, causal_scores_grouped + causal_softmax + causal_mix, {total:.1f} s of CPU work; "
+                      "pages gathered to contiguous outside the timing"}
+
+
 def main():
     a = parse()
     if a.gpus != 1:
@@ -386,7 +419,10 @@ def main():
             del w
         for n in (3, 4):
             w = W.CONFIGS[n](dev=dev)
-            secondary.append(bench_causal(w, dev, max(3, a.steps // 4), min(a.warmup, 2))[0])
+            line = bench_causal(w, dev, max(3, a.steps // 4), min(a.warmup, 2))[0]
+            if n == 4 and not a.no_cpu:
+                line["cpu_baseline"] = cpu_baseline_prefill(w, a.cpu_threads)
+            secondary.append(line)
             del w
         torch.cuda.empty_cache()
         for n in sorted([*W.TIERS, *W.WRITES, *W.LATENTS]):
