@@ -68,6 +68,8 @@ struct DecodeArgs {
 constexpr uint64_t kPlanAt = 64;
 uint64_t done_at(uint64_t rows) { return kPlanAt + 4 * (rows + 1); }
 uint64_t part_at(uint64_t rows, uint64_t units) { return (done_at(rows) + 4 * rows * units + 255) / 256 * 256; }
+// The grid of the shared-tile form: its XCD-aware order covers the splits in groups of 8.
+uint32_t shared_grid(uint64_t splits, uint64_t units) { return (uint32_t)((splits + 7) / 8 * 8 * units); }
 
 // Each row's split count, prefix-summed into plan[0..rows], and the counter zeroed. One workgroup. FUSED: also
 // the finished-split counts zeroed, and the answers of rows with no positions written as zeros (no split of
@@ -168,6 +170,13 @@ void decode_split(DecodeArgs a) {
     // the first item is the workgroup's own index; each next one comes from the counter (which counts past
     // the grid), asked for at the start of an item and read at its end so the atomic's trip is hidden
     uint32_t item = blockIdx.x;
+    if constexpr (SHARED && !PERSISTENT) {
+        // XCD-aware order: workgroups go to the 8 XCDs round robin (workgroup b to XCD b % 8), and the head blocks of
+        // one split read the same latents, so they take blocks 8·j + x for one x — one XCD and its L2 — and
+        // consecutive j. A block past the last split gets an item past the last and returns.
+        const uint32_t x = blockIdx.x & 7u, j = blockIdx.x >> 3;
+        item = ((j / GH) * 8u + x) * GH + j % GH;
+    }
     for (;;) {
     if (item >= total) break;
     uint32_t next = 0;
@@ -653,8 +662,9 @@ void decode_paged_launch(uint16_t* o, const uint16_t* q, const uint16_t* k, cons
     const bool shared = k == v;
     if (head_dim == 512) {
         if (shared) {
-            if (grouped) decode_split<512, 2, true, false, true><<<igrid, kThreads, 0, st>>>(a);
-            else decode_split<512, 2, false, false, true><<<igrid, kThreads, 0, st>>>(a);
+            const dim3 sgrid(shared_grid(rows * a.nsplit, kv_heads * a.hblocks));
+            if (grouped) decode_split<512, 2, true, false, true><<<sgrid, kThreads, 0, st>>>(a);
+            else decode_split<512, 2, false, false, true><<<sgrid, kThreads, 0, st>>>(a);
         } else {
             if (grouped) decode_split<512, 2, true, false><<<igrid, kThreads, 0, st>>>(a);
             else decode_split<512, 2, false, false><<<igrid, kThreads, 0, st>>>(a);
@@ -732,7 +742,7 @@ bool decode_one(uint16_t* o, float* res, const uint16_t* q, const uint16_t* k, c
     const dim3 grid((uint32_t)(nsplit * kv_heads * hblocks));
     prof_begin(kProfDecodeSplit);
     if (head_dim == 512) {
-        if (k == v) decode_split<512, 2, false, false, true><<<grid, kThreads, 0, st>>>(a);
+        if (k == v) decode_split<512, 2, false, false, true><<<dim3(shared_grid(nsplit, kv_heads * hblocks)), kThreads, 0, st>>>(a);
         else decode_split<512, 2, false, false><<<grid, kThreads, 0, st>>>(a);
     } else if (head_dim == 256) {
         decode_split<256, kDefaultVariant, false, false><<<grid, kThreads, 0, st>>>(a);
@@ -811,7 +821,8 @@ bool decode_causal(uint16_t* o, const uint16_t* q, const uint16_t* k, const uint
     const dim3 grid((uint32_t)(rows * a.nsplit * kv_heads * hblocks));
     prof_begin(kProfDecodeSplit);
     if (head_dim == 512) {
-        if (k == v) decode_split<512, 2, false, false, true><<<grid, kThreads, 0, st>>>(a);
+        if (k == v)
+            decode_split<512, 2, false, false, true><<<dim3(shared_grid(rows * a.nsplit, kv_heads * hblocks)), kThreads, 0, st>>>(a);
         else decode_split<512, 2, false, false><<<grid, kThreads, 0, st>>>(a);
     } else if (head_dim == 256) {
         decode_split<256, kDefaultVariant, false, false><<<grid, kThreads, 0, st>>>(a);
