@@ -81,6 +81,7 @@ def test_causal_residual_kernel(oracle, hd, qh, kvh, first, rows, ps):
 @pytest.mark.parametrize("qh,lens,ps,shared", [
     (64, [130, 41], 0, True),       # latent attention's shape: 64 heads, one kv head, keys = values, 512 wide
     (20, [97], 64, True),           # two head blocks, the second part-full; paged
+    (8, [70, 33], 16, True),        # pages shorter than a tile: one lookup a 16-key group
     (16, [130, 1], 0, False),       # head_dim 512 with values of their own
 ])
 def test_decode_head_dim_512(oracle, qh, lens, ps, shared):
