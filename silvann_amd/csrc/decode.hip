@@ -68,6 +68,9 @@ struct DecodeArgs {
 constexpr uint64_t kPlanAt = 64;
 uint64_t done_at(uint64_t rows) { return kPlanAt + 4 * (rows + 1); }
 uint64_t part_at(uint64_t rows, uint64_t units) { return (done_at(rows) + 4 * rows * units + 255) / 256 * 256; }
+// A launch's work-items (workgroups × 256) must stay below 2^32: the most workgroups a split grid may have.
+constexpr uint64_t kMaxGroups = (1ull << 32) / kThreads - 8;
+
 // The grid of the shared-tile form: its XCD-aware order covers the splits in groups of 8.
 uint32_t shared_grid(uint64_t splits, uint64_t units) { return (uint32_t)((splits + 7) / 8 * 8 * units); }
 
@@ -623,6 +626,10 @@ void decode_paged_launch(uint16_t* o, const uint16_t* q, const uint16_t* k, cons
     // as many workgroups as the chip holds at once (two a CU: LDS and registers allow no more), never more
     // than there are work items
     const uint64_t items = rows * a.nsplit * kv_heads * a.hblocks;   // at least the items there are
+    if (items + 8 * kv_heads * a.hblocks > kMaxGroups) {   // (the shared form rounds its splits up to 8)
+        refuse("attention_decode_paged");
+        return;
+    }
     const dim3 pgrid((uint32_t)(items < resident_groups() ? items : resident_groups()));
     const dim3 igrid((uint32_t)items);
     static const int mode = [] {
@@ -720,7 +727,7 @@ bool decode_one(uint16_t* o, float* res, const uint16_t* q, const uint16_t* k, c
     uint64_t chunk = choose_chunk(head_dim, kv_heads, hblocks, length, 1);
     if ((length + chunk - 1) / chunk > fit) chunk = ((length + fit - 1) / fit + step - 1) / step * step;
     const uint64_t nsplit = (length + chunk - 1) / chunk;
-    if (nsplit > fit || nsplit > kMaxSplits) return false;
+    if (nsplit > fit || nsplit > kMaxSplits || (nsplit + 8) * kv_heads * hblocks > kMaxGroups) return false;
     DecodeArgs a;
     a.q = q; a.k = k; a.v = v; a.pages = nullptr; a.pages_row = 0; a.page_size = 0; a.k_row = 0;
     a.q_heads = (uint32_t)q_heads; a.kv_heads = (uint32_t)kv_heads; a.group = (uint32_t)(q_heads / kv_heads);
@@ -801,7 +808,7 @@ bool decode_causal(uint16_t* o, const uint16_t* q, const uint16_t* k, const uint
     DecodeArgs a;
     a.chunk = (uint32_t)chunk;
     a.nsplit = (uint32_t)((most + chunk - 1) / chunk);
-    if (a.nsplit > fit || a.nsplit > kMaxSplits) return false;
+    if (a.nsplit > fit || a.nsplit > kMaxSplits || (rows * a.nsplit + 8) * kv_heads * hblocks > kMaxGroups) return false;
     a.q = q; a.k = k; a.v = v; a.pages = nullptr; a.pages_row = 0; a.page_size = 0; a.k_row = 0;
     a.q_heads = (uint32_t)q_heads; a.kv_heads = (uint32_t)kv_heads; a.group = (uint32_t)(q_heads / kv_heads);
     a.hblocks = hblocks;

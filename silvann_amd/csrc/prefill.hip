@@ -847,6 +847,10 @@ void causal_paged_launch(uint16_t* o, float* res, const uint16_t* q, const uint1
     // pair row tiles when the causal part dominates the work (a prefix shorter than the chunk)
     const bool paired = first < rows && a.rtiles > 1;
     const dim3 grid(paired ? (a.rtiles + 1) / 2 : a.rtiles, a.kv_heads * a.hblocks);
+    if ((uint64_t)grid.x * grid.y * kThreads >= (1ull << 32) || grid.y > 65535) {   // work-items below 2^32
+        refuse(what);
+        return;
+    }
     hipStream_t st = stream();
     prof_begin(kProfCausal);
     const bool ptl = pages && (first + rows + page_size - 1) / page_size <= kPagesInLds;
