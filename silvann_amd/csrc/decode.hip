@@ -27,6 +27,15 @@
 // K loads are 16 bytes a lane (8 halves of one key row: the MFMA A operand's own layout) into registers; V
 // goes straight from HBM into LDS (16 bytes a lane, consecutive lanes on consecutive bytes of a row), so it
 // takes no registers and two workgroups fit on a CU at head_dim 256.
+//
+// Other forms of the same kernels:
+//   head_dim 512     32-key tiles, one wave a SIMD; SHARED when k == v (latent attention: each tile comes into LDS
+//                    once and both operands are read from there), its workgroups in an XCD-aware order
+//   fused finish     (SILVANN_GFX950_DECODE_FUSED=1) the last split of a row and head block merges the others
+//   decode_one       one query of a deferred door pair (scores → mix, weights → residual_mix, the grouped chains
+//                    with a softmax or a sink), its scratch the pair's weights buffer; decode_merge_res writes the
+//                    residual, decode_merge<…, SINK> folds the sink in
+//   decode_causal    a deferred causal chain at head_dim 512: each row a decode over the same cache
 #include <math.h>
 #include <stdio.h>
 #include <stdlib.h>

@@ -13,8 +13,15 @@
 //   mix_rows      a workgroup per (row, kv head, 64 dims): 4 waves split the keys, a lane a dim, every query
 //                 head of the group accumulated from one read of each value; the waves meet in LDS
 //   merge/finish  a thread per head / per element.
-// The fused decode and causal rows (decode.hip, prefill.hip) are the fast paths; these doors are the
-// reference's contract for callers that read `p` or `res` themselves.
+// plus the TurboQuant rows' kernels (tq_scores, tq_mix_part, tq_mix_reduce) and softmax_sink_rows.
+//
+// The chains' first doors are deferred (common.hpp, `Deferred`): attention_scores, attention_weights,
+// attention_causal_scores_grouped, attention_scores_grouped, attention_weights_rows and the TurboQuant weights
+// doors record their operands instead of launching, and their continuation runs the chain as one fused kernel
+// (decode.hip, prefill.hip, tq_decode.hip) when it arrives with the same operands. Every other export here first
+// runs what is recorded (flush_deferred, below) with the bodies the deferred doors run on their own. These
+// kernels are then the reference's contract for every other order of calls, and for callers that read `p` or
+// `res` themselves.
 #include <math.h>
 #include <stdio.h>
 
