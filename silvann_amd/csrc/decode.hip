@@ -158,7 +158,9 @@ constexpr int kDefaultVariant = 2;
 // 128 registers a lane).
 // FUSED: the split that finishes last for its (row, kv head, head block) — it counts the finished splits — merges
 // them and writes the answers, as decode_merge does; no second launch.
-template <int HD, int VARIANT, bool GROUPED, bool PERSISTENT, bool SHARED = false, bool FUSED = false>
+// VTR: the V^T operand read with the transposing LDS read (two a MFMA) rather than element by element (eight) —
+// at head_dim 512, where the P·V MFMAs are the most a tile has.
+template <int HD, int VARIANT, bool GROUPED, bool PERSISTENT, bool SHARED = false, bool FUSED = false, bool VTR = (HD >= 512)>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(HD >= 512 ? 1 : 2, HD >= 512 ? 1 : 2)))
 void decode_split(DecodeArgs a) {
     constexpr int TK = tile_keys(HD);  // keys a wave takes a step: 32 KB of K and V whatever the head width
@@ -323,10 +325,23 @@ void decode_split(DecodeArgs a) {
             for (int n = 0; n < NT; ++n) {
                 const int d = 16 * n + col;
                 f16x8 va;
+                if constexpr (VTR) {
+                    // lane 4·jj + rr of 16-lane block grp points at key 32·sp + 4·grp + jj (+ 16), dims
+                    // 16·n + 4·rr .. +3; lane col of the block gets dim 16·n + col of its four keys
+                    const int li = lane & 15, jj = li >> 2, d0 = 16 * n + 4 * (li & 3);
+                    const int k0 = 32 * sp + 4 * grp + jj, k1 = k0 + 16;
+                    typedef short s16x4 __attribute__((ext_vector_type(4)));
+                    const s16x4 x0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                        (__attribute__((address_space(3))) s16x4*)(vs + (k0 * CPR + vslot(k0, d0 >> 3)) * 8 + (d0 & 7)));
+                    const s16x4 x1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                        (__attribute__((address_space(3))) s16x4*)(vs + (k1 * CPR + vslot(k1, d0 >> 3)) * 8 + (d0 & 7)));
+                    va = __builtin_bit_cast(f16x8, __builtin_shufflevector(x0, x1, 0, 1, 2, 3, 4, 5, 6, 7));
+                } else {
 #pragma unroll
-                for (int jj = 0; jj < 8; ++jj) {
-                    const int key = 32 * sp + (jj < 4 ? 4 * grp + jj : 16 + 4 * grp + (jj - 4));
-                    va[jj] = vs[(key * CPR + vslot(key, d >> 3)) * 8 + (d & 7)];
+                    for (int jj = 0; jj < 8; ++jj) {
+                        const int key = 32 * sp + (jj < 4 ? 4 * grp + jj : 16 + 4 * grp + (jj - 4));
+                        va[jj] = vs[(key * CPR + vslot(key, d >> 3)) * 8 + (d & 7)];
+                    }
                 }
                 acc[n] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va, pb[sp], acc[n], 0, 0, 0);
             }
