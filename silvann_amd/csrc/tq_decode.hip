@@ -15,7 +15,7 @@
 //             S^T       v_mfma_f32_16x16x32_f16, keys as M, the block's query heads as N
 //             softmax   online, in registers, as decode_split does
 //             V         decoded into the wave's LDS tile (fp16, rows swizzled in 16-byte chunks), then read
-//                       transposed as the A operand of O^T += V^T · P^T
+//                       with the transposing LDS read as the A operand of O^T += V^T · P^T
 //           then the four waves' (m, l, O) merge in LDS and the split's residual goes to the scratch.
 //   pass 2  tq_merge: a workgroup per (query row, query head, 64 dims) merges the splits exactly
 //           (kernels.cuh:1243-1255) into the residual res[h] = {m, l, acc}.
@@ -175,13 +175,17 @@ __global__ __launch_bounds__(kThreads) void tq_split(TqArgs a) {
         for (int sp = 0; sp < MT / 2; ++sp)
 #pragma unroll
             for (int n = 0; n < NT; ++n) {
-                const int d = 16 * n + col;
-                f16x8 va;
-#pragma unroll
-                for (int jj = 0; jj < 8; ++jj) {
-                    const int key = 32 * sp + (jj < 4 ? 4 * grp + jj : 16 + 4 * grp + (jj - 4));
-                    va[jj] = vt[(key * CPR + vslot(key, d >> 3)) * 8 + (d & 7)];
-                }
+                // V^T as the A operand through the transposing read: lane 4·jj + rr of 16-lane block grp points at
+                // key 32·sp + 4·grp + jj (+ 16), dims 16·n + 4·rr .. +3; lane col of the block gets dim 16·n + col
+                // of its four keys
+                const int li = lane & 15, jj = li >> 2, d0 = 16 * n + 4 * (li & 3);
+                const int k0 = 32 * sp + 4 * grp + jj, k1 = k0 + 16;
+                typedef short s16x4 __attribute__((ext_vector_type(4)));
+                const s16x4 x0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                    (__attribute__((address_space(3))) s16x4*)(vt + (k0 * CPR + vslot(k0, d0 >> 3)) * 8 + (d0 & 7)));
+                const s16x4 x1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                    (__attribute__((address_space(3))) s16x4*)(vt + (k1 * CPR + vslot(k1, d0 >> 3)) * 8 + (d0 & 7)));
+                const f16x8 va = __builtin_bit_cast(f16x8, __builtin_shufflevector(x0, x1, 0, 1, 2, 3, 4, 5, 6, 7));
                 acc[n] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va, pb[sp], acc[n], 0, 0, 0);
             }
         __builtin_amdgcn_s_waitcnt(0xC07F);   // lgkmcnt(0): this tile's reads are done before the next overwrites it
