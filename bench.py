@@ -429,6 +429,8 @@ def main():
             secondary.append(isolated(n, max(5, a.steps // 2), a.warmup))
         secondary.append(isolated(2, a.steps, a.warmup, env={"SILVANN_GFX950_DECODE_FUSED": "1"},
                                   variant="fused finish (no merge launch)"))
+        secondary.append(isolated(2, a.steps, a.warmup, env={"SILVANN_GFX950_DECODE_VTR": "1"},
+                                  variant="transposing V^T reads"))
         for n in (10, 11):
             secondary.append(isolated(n, max(5, a.steps // 2), a.warmup))
     cpu = None if a.no_cpu else cpu_baseline(w2, a.cpu_threads)

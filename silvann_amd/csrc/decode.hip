@@ -604,6 +604,14 @@ uint64_t resident_groups() {
     return groups;
 }
 
+bool vtr() {
+    static const bool on = [] {
+        const char* e = getenv("SILVANN_GFX950_DECODE_VTR");
+        return e && strtol(e, nullptr, 10) > 0;
+    }();
+    return on;
+}
+
 uint32_t head_blocks(uint64_t q_heads, uint64_t kv_heads) { return (uint32_t)((q_heads / kv_heads + 15) / 16); }
 
 bool decode_shape_ok(uint64_t q_heads, uint64_t kv_heads, uint64_t head_dim, uint64_t most, uint64_t rows) {
@@ -699,6 +707,19 @@ void decode_paged_launch(uint16_t* o, const uint16_t* q, const uint16_t* k, cons
         } else {
             if (grouped) decode_split<512, 2, true, false><<<igrid, kThreads, 0, st>>>(a);
             else decode_split<512, 2, false, false><<<igrid, kThreads, 0, st>>>(a);
+        }
+    } else if (vtr() && !persistent) {
+        // the transposing V^T read at head_dim <= 256 (SILVANN_GFX950_DECODE_VTR=1): checked in the CPU emulation,
+        // not yet measured against the element reads these widths run by default
+        switch (head_dim) {
+#define SILVANN_DECODE_VTR(HDV) \
+            case HDV: \
+                if (grouped) decode_split<HDV, kDefaultVariant, true, false, false, false, true><<<igrid, kThreads, 0, st>>>(a); \
+                else decode_split<HDV, kDefaultVariant, false, false, false, false, true><<<igrid, kThreads, 0, st>>>(a); \
+                break;
+            SILVANN_DECODE_VTR(64) SILVANN_DECODE_VTR(128) SILVANN_DECODE_VTR(256)
+#undef SILVANN_DECODE_VTR
+            default: break;
         }
     } else switch (head_dim * 4 + variant) {
 #define SILVANN_DECODE_CASE(HDV, VAR) \

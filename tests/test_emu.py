@@ -111,3 +111,19 @@ def test_decode_fused_finish(oracle, qh, kvh, hd, lens, ps):
                                   w.rows)
     parity(got, want)
     assert over == 0
+
+
+@pytest.mark.parametrize("qh,kvh,hd,lens,ps", [
+    (16, 2, 256, [700, 2048], 256),
+    (8, 2, 128, [1, 17, 300], 0),
+    (4, 4, 64, [33, 250], 16),
+])
+def test_decode_transposing_reads(oracle, qh, kvh, hd, lens, ps):
+    """Row 137 at head_dim <= 256 with the transposing V^T read (SILVANN_GFX950_DECODE_VTR=1, the candidate the
+    head_dim-512 kernels use) against the oracle."""
+    w = W.decode("emu", qh, kvh, hd, lens, page_size=ps, seed=hd + len(lens) + 7)
+    got, over, _ = emu.run_decode(w, env={"SILVANN_GFX950_DECODE_VTR": "1"})
+    want, _ = oracle.decode_paged(w.q, w.k, w.v, w.pages, w.pages_row, w.page_size, w.k_row, w.lens, qh, kvh, hd,
+                                  w.rows)
+    parity(got, want)
+    assert over == 0
