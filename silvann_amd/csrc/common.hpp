@@ -104,13 +104,15 @@ void refuse(const char* what);
 // attention_weights_tq then attention_residual_mix_tq (266-269, mixer__abi.cuh:395-407), the tiered prefill
 // window's many-row pairs (prefill__abi.cuh:430-440), and latent attention's attention_scores_grouped then
 // attention_softmax_rows (GLM 5.3, ai_z__glm_5_3/cpu/opcodes/layer__abi.cuh:283-289) or attention_softmax_sink
-// (DeepSeek V4, ai_deepseek_4/cpu/opcodes/layer__abi.cuh:299-301), then attention_mix. The first door of a
+// (DeepSeek V4, ai_deepseek_4/cpu/opcodes/layer__abi.cuh:299-301), then attention_mix, and its many-row form
+// attention_scores_grouped_rows, attention_softmax_lens, attention_mix_rows (GLM's block of rows, 1037-1043). The first door of a
 // chain is recorded, not launched; when its continuation arrives with the same operands the chain runs as one fused
 // kernel and the weights are never written. Any other door of this library first flushes what is recorded — runs
 // the recorded door as it would have run — so every other order keeps the reference's semantics.
 enum DeferKind : int {
     kDeferNone = 0, kDeferScores, kDeferWeights, kDeferCausal, kDeferCausalSoftmax, kDeferWeightsRows, kDeferWeightsTq,
-    kDeferWeightsTqRows, kDeferGrouped, kDeferGroupedSoftmax, kDeferGroupedSink
+    kDeferWeightsTqRows, kDeferGrouped, kDeferGroupedSoftmax, kDeferGroupedSink, kDeferGroupedRows,
+    kDeferGroupedRowsSoftmax
 };
 struct Deferred {
     int kind = kDeferNone;
@@ -121,6 +123,8 @@ struct Deferred {
     const uint8_t* codes = nullptr;   // TurboQuant key codes
     const uint16_t* scales = nullptr;
     const uint16_t* sink = nullptr;   // attention_softmax_sink's, one a head
+    const uint32_t* lens = nullptr;   // the many-row grouped chain's: rows' lengths, rows' strides
+    uint64_t p_row = 0, q_row = 0, k_row = 0;
     uint64_t q_heads = 0, kv_heads = 0, head_dim = 0, length = 0, first = 0, rows = 0, d = 0;
     hipStream_t st = nullptr;
 };
@@ -131,6 +135,9 @@ void flush_deferred();    // launch what is recorded, if anything, and clear it
 bool decode_one(uint16_t* o, float* res, const uint16_t* q, const uint16_t* k, const uint16_t* v, uint64_t q_heads,
                 uint64_t kv_heads, uint64_t head_dim, uint64_t length, void* scratch, uint64_t cap, unsigned int* over,
                 const uint16_t* sink = nullptr);
+bool decode_rows_fit(uint16_t* o, const uint16_t* q, const uint16_t* k, const uint16_t* v, const uint32_t* lens,
+                     uint64_t k_row, uint64_t q_heads, uint64_t kv_heads, uint64_t head_dim, uint64_t most,
+                     uint64_t rows, void* scratch, uint64_t cap, unsigned int* over);
 bool decode_causal(uint16_t* o, const uint16_t* q, const uint16_t* k, const uint16_t* v, uint64_t q_heads,
                    uint64_t kv_heads, uint64_t head_dim, uint64_t first, uint64_t rows, void* scratch, uint64_t cap,
                    unsigned int* over);

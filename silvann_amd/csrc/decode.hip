@@ -899,6 +899,70 @@ bool decode_causal(uint16_t* o, const uint16_t* q, const uint16_t* k, const uint
     return true;
 }
 
+// Rows over their own contiguous caches (row u's keys and values at k + u·k_row, lens[u] of them, lens on the device)
+// — the deferred many-row grouped chain's fused form (scores_grouped_rows + softmax_lens + mix_rows, GLM 5.3's
+// block of rows over their gathered latents). Its scratch is the chain's weights buffer, `cap` bytes, the split
+// length raised until the splits fit it. Answers false, launching nothing, when the shape is not one decode_split
+// takes or no split length fits.
+bool decode_rows_fit(uint16_t* o, const uint16_t* q, const uint16_t* k, const uint16_t* v, const uint32_t* lens,
+                     uint64_t k_row, uint64_t q_heads, uint64_t kv_heads, uint64_t head_dim, uint64_t most,
+                     uint64_t rows, void* scratch, uint64_t cap, unsigned int* over) {
+    if (!decode_shape_ok(q_heads, kv_heads, head_dim, most, rows) || (((uintptr_t)scratch) & 3u) != 0) return false;
+    const uint32_t hblocks = head_blocks(q_heads, kv_heads);
+    const uint64_t head = part_at(rows, kv_heads * hblocks);
+    const uint64_t per_split = rows * q_heads * (head_dim + 2) * sizeof(float);
+    if (cap <= head || (cap - head) / per_split == 0) return false;
+    const uint64_t fit = (cap - head) / per_split;   // splits a row the scratch holds
+    const uint64_t step = (uint64_t)tile_keys((int)head_dim) * kWaves;
+    uint64_t chunk = choose_chunk(head_dim, kv_heads, hblocks, most, rows);
+    if ((most + chunk - 1) / chunk > fit) chunk = ((most + fit - 1) / fit + step - 1) / step * step;
+    DecodeArgs a;
+    a.chunk = (uint32_t)chunk;
+    a.nsplit = (uint32_t)((most + chunk - 1) / chunk);
+    if (a.nsplit > fit || a.nsplit > kMaxSplits || (rows * a.nsplit + 8) * kv_heads * hblocks > kMaxGroups) return false;
+    a.q = q; a.k = k; a.v = v; a.pages = nullptr; a.pages_row = 0; a.page_size = 0; a.k_row = k_row;
+    a.lens = lens;
+    a.q_heads = (uint32_t)q_heads; a.kv_heads = (uint32_t)kv_heads; a.group = (uint32_t)(q_heads / kv_heads);
+    a.hblocks = hblocks;
+    a.scale = 1.0f / sqrtf((float)head_dim);
+    a.counter = (uint32_t*)scratch;
+    a.plan = (const uint32_t*)((char*)scratch + kPlanAt);
+    a.done = (uint32_t*)((char*)scratch + done_at(rows));
+    a.part = (float*)((char*)scratch + head);
+    a.rows = (uint32_t)rows;
+    a.o = o;
+    a.over = over;
+    hipStream_t st = stream();
+    decode_plan<<<1, 256, 0, st>>>(lens, a.rows, a.chunk, (uint32_t*)a.plan, a.counter);
+    const dim3 grid((uint32_t)(rows * a.nsplit * kv_heads * hblocks));
+    prof_begin(kProfDecodeSplit);
+    if (head_dim == 512) {
+        if (k == v)
+            decode_split<512, 2, false, false, true><<<dim3(shared_grid(rows * a.nsplit, kv_heads * hblocks)), kThreads, 0, st>>>(a);
+        else decode_split<512, 2, false, false><<<grid, kThreads, 0, st>>>(a);
+    } else if (head_dim == 256) {
+        decode_split<256, kDefaultVariant, false, false><<<grid, kThreads, 0, st>>>(a);
+    } else if (head_dim == 128) {
+        decode_split<128, kDefaultVariant, false, false><<<grid, kThreads, 0, st>>>(a);
+    } else {
+        decode_split<64, kDefaultVariant, false, false><<<grid, kThreads, 0, st>>>(a);
+    }
+    prof_end(kProfDecodeSplit);
+    const dim3 mgrid((uint32_t)q_heads, (uint32_t)rows, (uint32_t)(head_dim / 64));
+    const bool wide = a.nsplit > 64;
+#define SILVANN_MERGE_R(HDV) \
+    if (wide) decode_merge<HDV, 16><<<mgrid, 1024, 0, st>>>(o, a.part, lens, a.q_heads, a.chunk, a.nsplit, over, nullptr); \
+    else decode_merge<HDV, 4><<<mgrid, 256, 0, st>>>(o, a.part, lens, a.q_heads, a.chunk, a.nsplit, over, nullptr);
+    switch (head_dim) {
+        case 64: SILVANN_MERGE_R(64) break;
+        case 128: SILVANN_MERGE_R(128) break;
+        case 256: SILVANN_MERGE_R(256) break;
+        default: SILVANN_MERGE_R(512) break;
+    }
+#undef SILVANN_MERGE_R
+    return true;
+}
+
 uint64_t decode_paged_scratch(uint64_t q_heads, uint64_t kv_heads, uint64_t head_dim, uint64_t most, uint64_t rows) {
     if (!decode_shape_ok(q_heads, kv_heads, head_dim, most, rows)) return 0;
     const uint32_t chunk = choose_chunk(head_dim, kv_heads, head_blocks(q_heads, kv_heads), most, rows);

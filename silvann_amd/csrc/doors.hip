@@ -641,6 +641,24 @@ void softmax_sink_body(float* p, const uint16_t* sink, uint64_t rows, uint64_t l
     check_launch("attention_softmax_sink");
 }
 
+void scores_grouped_rows_body(float* p, uint64_t p_row, const uint16_t* q, uint64_t q_row, const uint16_t* k,
+                              uint64_t k_row, const uint32_t* lens, uint64_t q_heads, uint64_t kv_heads,
+                              uint64_t head_dim, uint64_t most, uint64_t rows) {
+    if (!heads_ok("attention_scores_grouped_rows", q_heads, kv_heads, head_dim, rows)) return;
+    Geom G = geom(kLens, q_heads, kv_heads, head_dim);
+    G.p_row = p_row; G.q_row = q_row; G.k_row = k_row; G.lens = lens;
+    launch_scores(p, q, k, G, rows, most);
+    check_launch("attention_scores_grouped_rows");
+}
+
+void softmax_lens_body(float* p, uint64_t p_row, const uint32_t* lens, uint64_t heads, uint64_t rows) {
+    if (heads == 0) return;
+    Geom G = geom(kLens, heads, 1, 1);
+    G.p_row = p_row; G.lens = lens;
+    launch_softmax(p, nullptr, G, rows * heads);
+    check_launch("attention_softmax_lens");
+}
+
 // A door records its chain's first step only when a fused form could take the chain (and the shape is valid:
 // an invalid one runs at once, to be refused).
 bool decode_chain_shape(uint64_t q_heads, uint64_t kv_heads, uint64_t head_dim, uint64_t length) {
@@ -679,6 +697,15 @@ void flush_deferred() {
         case kDeferGroupedSink:
             scores_grouped_body(r.p, r.q, r.k, r.q_heads, r.kv_heads, r.head_dim, r.length);
             softmax_sink_body(r.p, r.sink, r.q_heads, r.length);
+            break;
+        case kDeferGroupedRows:
+            scores_grouped_rows_body(r.p, r.p_row, r.q, r.q_row, r.k, r.k_row, r.lens, r.q_heads, r.kv_heads,
+                                     r.head_dim, r.length, r.rows);
+            break;
+        case kDeferGroupedRowsSoftmax:
+            scores_grouped_rows_body(r.p, r.p_row, r.q, r.q_row, r.k, r.k_row, r.lens, r.q_heads, r.kv_heads,
+                                     r.head_dim, r.length, r.rows);
+            softmax_lens_body(r.p, r.p_row, r.lens, r.q_heads, r.rows);
             break;
         case kDeferWeightsTqRows:
             weights_tq_rows_body(r.p, r.res, r.q, r.codes, r.scales, r.q_heads, r.kv_heads, r.head_dim, r.length, r.d,
@@ -938,23 +965,29 @@ SILVANN_EXPORT void silvann_gfx950_attention_scores_grouped_rows(float* p, uint6
                                                                  const uint32_t* lens, uint64_t q_heads,
                                                                  uint64_t kv_heads, uint64_t head_dim, uint64_t most,
                                                                  uint64_t rows) {
-    silvann::flush_deferred();
-    if (!heads_ok("attention_scores_grouped_rows", q_heads, kv_heads, head_dim, rows)) return;
-    Geom G = geom(kLens, q_heads, kv_heads, head_dim);
-    G.p_row = p_row; G.q_row = q_row; G.k_row = k_row; G.lens = lens;
-    launch_scores(p, q, k, G, rows, most);
-    check_launch("attention_scores_grouped_rows");
+    flush_deferred();
+    if (defer_enabled() && decode_chain_shape(q_heads, kv_heads, head_dim, most) && rows > 0 && rows <= 65535 &&
+        q_row == q_heads * head_dim) {
+        Deferred& d = deferred();   // with softmax_lens and mix_rows: the split-K decode of every row
+        d.kind = kDeferGroupedRows; d.p = p; d.p_row = p_row; d.q = q; d.q_row = q_row; d.k = k; d.k_row = k_row;
+        d.lens = lens; d.q_heads = q_heads; d.kv_heads = kv_heads; d.head_dim = head_dim; d.length = most;
+        d.rows = rows; d.st = stream();
+        return;
+    }
+    scores_grouped_rows_body(p, p_row, q, q_row, k, k_row, lens, q_heads, kv_heads, head_dim, most, rows);
 }
 
 // gpu.cuh:223 — kernels.cuh:1104-1110
 SILVANN_EXPORT void silvann_gfx950_attention_softmax_lens(float* p, uint64_t p_row, const uint32_t* lens,
                                                           uint64_t heads, uint64_t rows) {
-    silvann::flush_deferred();
-    if (heads == 0) return;
-    Geom G = geom(kLens, heads, 1, 1);
-    G.p_row = p_row; G.lens = lens;
-    launch_softmax(p, nullptr, G, rows * heads);
-    check_launch("attention_softmax_lens");
+    Deferred& d = deferred();
+    if (d.kind == kDeferGroupedRows && d.p == p && d.p_row == p_row && d.lens == lens && d.q_heads == heads &&
+        d.rows == rows && d.st == stream()) {
+        d.kind = kDeferGroupedRowsSoftmax;   // the chain's second step, recorded too
+        return;
+    }
+    flush_deferred();
+    softmax_lens_body(p, p_row, lens, heads, rows);
 }
 
 // gpu.cuh:224 — kernels.cuh:1169-1178
@@ -962,7 +995,17 @@ SILVANN_EXPORT void silvann_gfx950_attention_mix_rows(uint16_t* o, uint64_t o_ro
                                                       const uint16_t* v, uint64_t v_row, const uint32_t* lens,
                                                       uint64_t q_heads, uint64_t kv_heads, uint64_t head_dim,
                                                       uint64_t rows, unsigned int* over) {
-    silvann::flush_deferred();
+    Deferred& d = deferred();
+    if (d.kind == kDeferGroupedRowsSoftmax && d.p == p && d.p_row == p_row && d.lens == lens &&
+        d.q_heads == q_heads && d.kv_heads == kv_heads && d.head_dim == head_dim && d.rows == rows &&
+        o_row == q_heads * head_dim && v_row == d.k_row && d.st == stream() &&
+        decode_rows_fit(o, d.q, d.k, v, lens, d.k_row, q_heads, kv_heads, head_dim, d.length, rows,
+                        const_cast<float*>(p), rows * p_row * sizeof(float), over)) {
+        d = Deferred();   // the chain ran fused: p holds the splits' residuals, not weights
+        check_launch("attention_mix_rows");
+        return;
+    }
+    flush_deferred();
     if (!heads_ok("attention_mix_rows", q_heads, kv_heads, head_dim, rows)) return;
     Geom G = geom(kLens, q_heads, kv_heads, head_dim);
     G.p_row = p_row; G.k_row = v_row; G.o_row = o_row; G.lens = lens;

@@ -195,3 +195,12 @@ def run_chain_grouped(q, k, v, qh, kvh, hd, length, sink=None, interleave=False,
     if sink is not None:
         files["lens"] = np.ascontiguousarray(sink, np.uint16)
     return _run(files, params, None, timeout, outs=(("o", np.float16), ("p", np.float32)))
+
+
+def run_chain_grouped_rows(q, lat, lens, qh, hd, most, interleave=False, timeout: int = 900):
+    """GLM's block chain: attention_scores_grouped_rows, attention_softmax_lens, attention_mix_rows, one kv head, row u
+    over its own `lens[u]` latents at lat + u·most·hd (keys and values). The answers, the weights buffer afterwards
+    and the fault word."""
+    params = f"chain_grows {qh} 1 {hd} {most} {len(lens)} {1 if interleave else 0} 0 {most * hd}"
+    return _run({"q": q, "k": lat, "lens": np.ascontiguousarray(lens, np.uint32)}, params, None, timeout,
+                outs=(("o", np.float16), ("p", np.float32)))

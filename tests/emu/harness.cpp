@@ -250,6 +250,28 @@ int main(int argc, char** argv) {
         save(d + "/over.bin", over, 4);
         fprintf(stderr, "emu done: refused %d, wave exchanges %ld\n", silvann::emu_refused, (long)emu::ops);
         return silvann::emu_refused ? 5 : 0;
+    } else if (std::string(mode) == "chain_grows") {
+        // scores_grouped_rows, softmax_lens, mix_rows: a1 rows over their own lens (lens.bin) of at most a0 keys, at
+        // k + u·k_row; ps = 1 puts another door between the softmax and the mix
+        const unsigned long rows = a1, most = a0, p_row = qh * most, o_row = qh * hd;
+        char* lens = load(d + "/lens.bin", "lens");
+        float* p = (float*)guarded(rows * p_row * 4, "p");
+        memset(p, 0xFF, rows * p_row * 4);
+        const unsigned long on = rows * o_row * 2;
+        uint16_t* o16 = (uint16_t*)guarded(on, "o");
+        memset(o16, 0xFF, on);
+        silvann_gfx950_attention_scores_grouped_rows(p, p_row, (const uint16_t*)q, o_row, (const uint16_t*)k, k_row,
+                                                     (const uint32_t*)lens, qh, kvh, hd, most, rows);
+        silvann_gfx950_attention_softmax_lens(p, p_row, (const uint32_t*)lens, qh, rows);
+        if (ps == 1) silvann_gfx950_attention_finish(nullptr, nullptr, 0, hd, over);
+        silvann_gfx950_attention_mix_rows(o16, o_row, p, p_row, (const uint16_t*)v, k_row, (const uint32_t*)lens, qh,
+                                          kvh, hd, rows, over);
+        silvann_gfx950_flush();
+        save(d + "/o.bin", o16, on);
+        save(d + "/p.bin", p, rows * p_row * 4);
+        save(d + "/over.bin", over, 4);
+        fprintf(stderr, "emu done: refused %d, wave exchanges %ld\n", silvann::emu_refused, (long)emu::ops);
+        return silvann::emu_refused ? 5 : 0;
     } else if (std::string(mode) == "chain_causal") {
         // causal_scores_grouped, causal_softmax, causal_mix from a0 = first over a1 = rows, as nn__attention__rows
         // calls them; ps = 1 puts another door (a finish of nothing) between the softmax and the mix

@@ -153,3 +153,27 @@ def test_grouped_chain(oracle, qh, hd, length, sink, interleave, fused):
         assert not np.allclose(p, wp, rtol=1e-4, atol=1e-6)
     else:
         np.testing.assert_allclose(p, wp, rtol=1e-4, atol=1e-6)
+
+
+@pytest.mark.parametrize("interleave,fused", [(False, True), (True, False)])
+def test_grouped_rows_chain(oracle, interleave, fused):
+    """GLM 5.3's block of rows over their gathered latents (layer__abi.cuh:1037-1043): scores_grouped_rows,
+    softmax_lens, mix_rows as one split-K decode of every row, the weights buffer its scratch."""
+    qh, hd, lens = 16, 512, [1100, 1, 700]
+    most, rows = max(lens), len(lens)
+    rng = np.random.default_rng(11 + interleave)
+    q = rng.standard_normal(rows * qh * hd).astype(np.float16)
+    lat = rng.standard_normal(rows * most * hd).astype(np.float16)
+    lens_np = np.asarray(lens, np.uint32)
+    o, p, over, _ = emu.run_chain_grouped_rows(q, lat, lens_np, qh, hd, most, interleave=interleave)
+    p_row = qh * most
+    raw = oracle.scores_grouped_rows(p_row, q, qh * hd, lat, most * hd, lens_np, qh, 1, hd, most, rows)
+    wp = oracle.softmax_lens(raw, p_row, lens_np, qh, rows)
+    want, _ = oracle.mix_rows(qh * hd, wp, p_row, lat, most * hd, lens_np, qh, 1, hd, rows)
+    parity(o, want)
+    assert over == 0
+    valid = np.concatenate([np.r_[np.ones(qh * n, bool), np.zeros(p_row - qh * n, bool)] for n in lens])
+    if fused:
+        assert not np.allclose(p[valid], wp[valid], rtol=1e-4, atol=1e-6)
+    else:
+        np.testing.assert_allclose(p[valid], wp[valid], rtol=1e-4, atol=1e-6)

@@ -42,7 +42,8 @@ def test_latent_attention(dev, oracle, heads, hd, lens):
     got = out.cpu().numpy()
     parity(got, want)
     assert not doors.launch_failed()
-    # the library's generic doors in the reference's order agree too
+    # the library's generic doors in the reference's order, each on its own, agree too
+    doors.set_defer(False)
     qd, ld, lnd = t(q, dev), t(lat, dev), t(lens_np, dev)
     p = torch.zeros(rows * heads * most, dtype=torch.float32, device=dev)
     o2 = torch.zeros_like(out)
@@ -50,5 +51,35 @@ def test_latent_attention(dev, oracle, heads, hd, lens):
     doors.attention_scores_grouped_rows(p, heads * most, qd, heads * hd, ld, most * hd, lnd, heads, 1, hd, most, rows)
     doors.attention_softmax_lens(p, heads * most, lnd, heads, rows)
     doors.attention_mix_rows(o2, heads * hd, p, heads * most, ld, most * hd, lnd, heads, 1, hd, rows, over)
+    doors.set_defer(True)
     parity(got, o2.cpu().numpy())
     assert int(over.item()) == 0
+
+
+def test_block_chain_runs_fused(dev, oracle):
+    """The same doors called as GLM's block prefill calls them (layer__abi.cuh:1037-1043), deferral on: the chain
+    runs as one split-K decode of every row, the weights buffer its scratch."""
+    heads, hd, lens = 64, 512, [2048, 1, 1500, 2048]
+    print("case: latent block chain", flush=True)
+    rng = np.random.default_rng(5)
+    rows, most = len(lens), max(lens)
+    q = rng.standard_normal(rows * heads * hd).astype(np.float16)
+    lat = rng.standard_normal(rows * most * hd).astype(np.float16)
+    lens_np = np.asarray(lens, np.uint32)
+    want = _oracle(oracle, q, lat, lens_np, heads, hd, most)
+    qd, ld, lnd = t(q, dev), t(lat, dev), t(lens_np, dev)
+    p = torch.zeros(rows * heads * most, dtype=torch.float32, device=dev)
+    o = torch.zeros(rows * heads * hd, dtype=torch.float16, device=dev)
+    over = torch.zeros(1, dtype=torch.int32, device=dev)
+    doors.set_defer(True)
+    doors.attention_scores_grouped_rows(p, heads * most, qd, heads * hd, ld, most * hd, lnd, heads, 1, hd, most, rows)
+    doors.attention_softmax_lens(p, heads * most, lnd, heads, rows)
+    doors.attention_mix_rows(o, heads * hd, p, heads * most, ld, most * hd, lnd, heads, 1, hd, rows, over)
+    parity(o.cpu().numpy(), want)
+    assert int(over.item()) == 0
+    p_row = heads * most
+    wp = oracle.softmax_lens(oracle.scores_grouped_rows(p_row, q, heads * hd, lat, most * hd, lens_np, heads, 1, hd, most,
+                                                        rows), p_row, lens_np, heads, rows)
+    # fused: the buffer held the splits' scratch, not the weights
+    assert not np.allclose(p.cpu().numpy()[: heads * lens[0]], wp[: heads * lens[0]], rtol=1e-4, atol=1e-6)
+    assert not doors.launch_failed()
