@@ -48,6 +48,10 @@ def build() -> Path:
         raise RuntimeError("no clang++ for the emulation")
     key = _digest()
     exe = BUILD / f"emu-{key}"
+    if BUILD.exists():
+        for old in BUILD.glob("*"):   # builds of earlier sources
+            if (old.name.startswith("emu-") or old.suffix == ".o") and key not in old.name:
+                old.unlink(missing_ok=True)
     if exe.exists():
         return exe
     srcs = gen.write(BUILD, SOURCES) + [HERE / "harness.cpp"]
