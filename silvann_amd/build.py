@@ -1,6 +1,7 @@
-"""Build the gfx950 attention library in-tree: silvann_amd/libsilvann_gfx950_attention.so.
+"""Build the gfx950 attention library in-tree: silvann_amd/libsilvann_gfx950_attention.so, and the same objects as a
+SiLVANN silicon family of their own, silvann_amd/libsilvann_gfx950_family.so.
 
-One hipcc invocation a source file (in parallel), then one link. Every HIP source is compiled for gfx950
+One hipcc invocation a source file (in parallel), then one link a library. Every HIP source is compiled for gfx950
 only, with packed-fp32 instruction selection switched off (the pool's rule for these boxes) and every
 symbol hidden except the `extern "C"` entry points include/silvann_gfx950_attention.h declares.
 """
@@ -16,6 +17,7 @@ PKG = Path(__file__).resolve().parent
 CSRC = PKG / "csrc"
 BUILD = PKG / "_build"
 LIB = PKG / "libsilvann_gfx950_attention.so"
+FAMILY = PKG / "libsilvann_gfx950_family.so"
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 
 FLAGS = [
@@ -26,7 +28,7 @@ FLAGS = [
 
 
 def _compile(src: Path) -> Path:
-    obj = BUILD / (src.stem + ".o")
+    obj = BUILD / (src.parent.name + "_" + src.stem + ".o" if src.parent != CSRC else src.stem + ".o")
     cmd = [HIPCC, *FLAGS, "-c", str(src), "-o", str(obj)]
     r = subprocess.run(cmd, capture_output=True, text=True)
     noise = "is not a recognized feature for this target"
@@ -38,21 +40,29 @@ def _compile(src: Path) -> Path:
     return obj
 
 
+def _link(objs: list[Path], out: Path, extra: list[str]) -> None:
+    tmp = out.with_suffix(".so.tmp")
+    cmd = [HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", *map(str, objs), *extra, "-o", str(tmp)]
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError(f"link of {out.name} failed:\n" + r.stdout + r.stderr)
+    os.replace(tmp, out)
+
+
 def build(verbose: bool = True) -> Path:
     BUILD.mkdir(exist_ok=True)
     sources = sorted(CSRC.glob("*.hip"))
-    with cf.ThreadPoolExecutor(max_workers=min(8, len(sources))) as ex:
-        objs = list(ex.map(_compile, sources))
-    tmp = LIB.with_suffix(".so.tmp")
-    cmd = [HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", *map(str, objs), "-o", str(tmp)]
-    r = subprocess.run(cmd, capture_output=True, text=True)
-    if r.returncode != 0:
-        raise RuntimeError("link failed:\n" + r.stdout + r.stderr)
-    os.replace(tmp, LIB)
+    family = sorted((CSRC / "family").glob("*.hip"))
+    with cf.ThreadPoolExecutor(max_workers=min(8, len(sources) + len(family))) as ex:
+        objs = list(ex.map(_compile, sources + family))
+    lib_objs, family_objs = objs[:len(sources)], objs[len(sources):]
+    _link(lib_objs, LIB, [])
+    # the family: the same objects and its entry point, every other name local
+    _link(lib_objs + family_objs, FAMILY, [f"-Wl,--version-script={CSRC / 'family' / 'family.map'}"])
     if verbose:
-        print(f"built {LIB.relative_to(PKG.parent)} from {len(sources)} sources")
+        print(f"built {LIB.relative_to(PKG.parent)} from {len(sources)} sources, "
+              f"{FAMILY.relative_to(PKG.parent)} with the family entry point")
     return LIB
-
 
 if __name__ == "__main__":
     build()
