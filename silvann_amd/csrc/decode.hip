@@ -160,9 +160,11 @@ constexpr int kDefaultVariant = 2;
 // them and writes the answers, as decode_merge does; no second launch.
 // VTR: the V^T operand read with the transposing LDS read (two a MFMA) rather than element by element (eight) —
 // at head_dim 512, where the P·V MFMAs are the most a tile has.
-template <int HD, int VARIANT, bool GROUPED, bool PERSISTENT, bool SHARED = false, bool FUSED = false, bool VTR = (HD >= 512)>
+template <int HD, int VARIANT, bool GROUPED, bool PERSISTENT, bool SHARED = false, bool FUSED = false, bool VTR = (HD >= 512),
+          bool INLINE = false>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(HD >= 512 ? 1 : 2, HD >= 512 ? 1 : 2)))
 void decode_split(DecodeArgs a) {
+    static_assert(!INLINE || (!PERSISTENT && !FUSED), "the inline plan is for one workgroup an item, merged apart");
     constexpr int TK = tile_keys(HD);  // keys a wave takes a step: 32 KB of K and V whatever the head width
     constexpr int MT = TK / 16;      // 16-key M tiles of S^T
     constexpr int KS = HD / 32;      // k-steps of the S^T MFMA (32 dims each)
@@ -178,7 +180,24 @@ void decode_split(DecodeArgs a) {
     const int col = lane & 15, grp = lane >> 4;
     const uint64_t row = (uint64_t)a.kv_heads * HD;
     const uint32_t GH = a.kv_heads * a.hblocks;
-    const uint32_t total = a.plan[a.rows] * GH;
+    // INLINE (at most 64 rows): every wave makes the plan itself — lane u holds row u's length and the splits of the
+    // rows before it (a butterfly scan), and an item's row is the last lane whose splits-before are at most its
+    // split index — so no plan launch goes first.
+    uint32_t lane_len = 0, lane_before = 0, inline_total = 0;
+    if constexpr (INLINE) {
+        lane_len = lane < (int)a.rows ? a.lens[lane] : 0u;
+        const uint32_t n = (lane_len + a.chunk - 1) / a.chunk;
+        uint32_t incl = n, sum = n;
+#pragma unroll
+        for (int b = 1; b < 64; b <<= 1) {
+            const uint32_t t = __shfl_xor(sum, b);
+            if (lane & b) incl += t;
+            sum += t;
+        }
+        lane_before = incl - n;
+        inline_total = __builtin_amdgcn_readfirstlane(sum) * GH;
+    }
+    const uint32_t total = INLINE ? inline_total : a.plan[a.rows] * GH;
     __shared__ uint32_t item_at;
     __shared__ uint32_t is_last;
     // the first item is the workgroup's own index; each next one comes from the counter (which counts past
@@ -197,14 +216,19 @@ void decode_split(DecodeArgs a) {
     if (PERSISTENT && threadIdx.x == 0) next = gridDim.x + atomicAdd(a.counter, 1u);
     const uint32_t sidx = item / GH, gh = item % GH;
     uint32_t lo = 0, hi = a.rows;
-    while (hi - lo > 1) {
-        const uint32_t mid = (lo + hi) >> 1;
-        if (a.plan[mid] <= sidx) lo = mid;
-        else hi = mid;
+    if constexpr (INLINE) {
+        // lane 0 (no splits before it) always counts, so lo is a row
+        lo = (uint32_t)__builtin_popcountll(__builtin_amdgcn_ballot_w64(lane < (int)a.rows && lane_before <= sidx)) - 1u;
+    } else {
+        while (hi - lo > 1) {
+            const uint32_t mid = (lo + hi) >> 1;
+            if (a.plan[mid] <= sidx) lo = mid;
+            else hi = mid;
+        }
     }
-    const uint32_t u = lo, s = sidx - a.plan[lo];
+    const uint32_t u = lo, s = sidx - (INLINE ? (uint32_t)__builtin_amdgcn_readlane((int)lane_before, (int)lo) : a.plan[lo]);
     const uint32_t g = gh / a.hblocks, hb = gh % a.hblocks;
-    const uint32_t len = a.lens[u];
+    const uint32_t len = INLINE ? (uint32_t)__builtin_amdgcn_readlane((int)lane_len, (int)u) : a.lens[u];
     const uint32_t start = s * a.chunk;
     const uint32_t end = min(len, start + a.chunk);
     const uint32_t h0 = g * a.group + hb * 16;
@@ -695,7 +719,14 @@ void decode_paged_launch(uint16_t* o, const uint16_t* q, const uint16_t* k, cons
         check_launch("attention_decode_paged");
         return;
     }
-    decode_plan<<<1, 256, 0, st>>>(lens, a.rows, a.chunk, (uint32_t*)a.plan, a.counter);
+    // the plan made inside decode_split (SILVANN_GFX950_DECODE_INLINE=1, batches of at most 64 rows): one launch
+    // fewer a step; checked in the CPU emulation, not yet measured on a GPU
+    static const bool inline_plan = [] {
+        const char* e = getenv("SILVANN_GFX950_DECODE_INLINE");
+        return e && strtol(e, nullptr, 10) > 0;
+    }();
+    const bool inlined = inline_plan && rows <= 64 && head_dim <= 256 && !persistent && !vtr();
+    if (!inlined) decode_plan<<<1, 256, 0, st>>>(lens, a.rows, a.chunk, (uint32_t*)a.plan, a.counter);
     prof_begin(kProfDecodeSplit);
     // head_dim 512: one workgroup an item; the shared-tile form when the keys are the values
     const bool shared = k == v;
@@ -707,6 +738,17 @@ void decode_paged_launch(uint16_t* o, const uint16_t* q, const uint16_t* k, cons
         } else {
             if (grouped) decode_split<512, 2, true, false><<<igrid, kThreads, 0, st>>>(a);
             else decode_split<512, 2, false, false><<<igrid, kThreads, 0, st>>>(a);
+        }
+    } else if (inlined) {
+        switch (head_dim) {
+#define SILVANN_DECODE_INLINE(HDV) \
+            case HDV: \
+                if (grouped) decode_split<HDV, kDefaultVariant, true, false, false, false, false, true><<<igrid, kThreads, 0, st>>>(a); \
+                else decode_split<HDV, kDefaultVariant, false, false, false, false, false, true><<<igrid, kThreads, 0, st>>>(a); \
+                break;
+            SILVANN_DECODE_INLINE(64) SILVANN_DECODE_INLINE(128) SILVANN_DECODE_INLINE(256)
+#undef SILVANN_DECODE_INLINE
+            default: break;
         }
     } else if (vtr() && !persistent) {
         // the transposing V^T read at head_dim <= 256 (SILVANN_GFX950_DECODE_VTR=1): checked in the CPU emulation,

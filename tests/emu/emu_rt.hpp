@@ -71,7 +71,9 @@ inline void waitcnt(int imm) {
     while (tl_dma.size() - tl_dma_head > vm) { auto& p = tl_dma[tl_dma_head++]; std::memcpy(p.dst, p.data, 16); }
     if (tl_dma_head == tl_dma.size()) { tl_dma.clear(); tl_dma_head = 0; }
 }
-inline void launch(dim3 grid, uint32_t threads, std::function<void()> body) {
+inline void launch(dim3 grid, uint32_t threads, std::function<void()> body, const char* name = "") {
+    static const bool log = getenv("EMU_LAUNCHES") != nullptr;
+    if (log) std::fprintf(stderr, "emu launch %s\n", name);
     gridDim = {grid.x, grid.y, grid.z};
     blockDim = {threads, 1, 1};
     const int nw = (threads + 63) / 64;
@@ -122,6 +124,9 @@ template <class T> inline T emu_readfirstlane(T v) {
 #define __builtin_amdgcn_readfirstlane(v) emu_readfirstlane(v)
 inline uint64_t __builtin_amdgcn_ballot_w64(bool p) {
     return emu::wave_op(p, [](auto get) { uint64_t m = 0; for (int l = 0; l < 64; ++l) if (get(l)) m |= 1ull << l; return m; });
+}
+inline int __builtin_amdgcn_readlane(int v, int l) {
+    return emu::wave_op(v, [&](auto get) { return get(l); });
 }
 template <class T> inline T __shfl_xor(T v, int mask, int width = 64) {
     const int me = emu::tl_lane;

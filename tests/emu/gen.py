@@ -111,7 +111,8 @@ def _launches(s: str) -> str:
                     break
             m += 1
         out.append(s[i:k])
-        out.append(f"emu::launch({cfg[0]}, {cfg[1]}, [&]{{ {s[k:j]}{s[e + 3:m + 1]}; }})")
+        name = " ".join(s[k:j].split())
+        out.append(f"emu::launch({cfg[0]}, {cfg[1]}, [&]{{ {s[k:j]}{s[e + 3:m + 1]}; }}, \"{name}\")")
         i = m + 1
 
 

@@ -127,3 +127,24 @@ def test_decode_transposing_reads(oracle, qh, kvh, hd, lens, ps):
                                   w.rows)
     parity(got, want)
     assert over == 0
+
+
+INLINE = {"SILVANN_GFX950_DECODE_INLINE": "1", "EMU_LAUNCHES": "1"}
+
+
+@pytest.mark.parametrize("qh,kvh,hd,lens,ps", [
+    (16, 2, 256, [700, 0, 2048, 0], 256),                  # empty rows between and last
+    (8, 2, 128, [0, 1, 17, 3000, 5], 0),                   # an empty first row; many splits beside one-split rows
+    (4, 4, 64, [(37 * i) % 300 for i in range(64)], 16),   # 64 rows (the inline plan's most), pages shorter than a tile
+])
+def test_decode_inline_plan(oracle, qh, kvh, hd, lens, ps):
+    """Row 137 with its plan made inside decode_split (SILVANN_GFX950_DECODE_INLINE=1: each wave's prefix scan of
+    the rows' split counts, an item's row found by ballot) against the oracle, with no plan launch."""
+    w = W.decode("emu", qh, kvh, hd, lens, page_size=ps, seed=hd + len(lens) + 11)
+    got, over, log = emu.run_decode(w, env=INLINE)
+    want, _ = oracle.decode_paged(w.q, w.k, w.v, w.pages, w.pages_row, w.page_size, w.k_row, w.lens, qh, kvh, hd,
+                                  w.rows)
+    parity(got, want)
+    assert over == 0
+    launched = [ln for ln in log.splitlines() if ln.startswith("emu launch ")]
+    assert len(launched) == 2 and "decode_split" in launched[0] and "decode_merge" in launched[1], launched

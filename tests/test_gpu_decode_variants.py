@@ -1,0 +1,33 @@
+"""Row 137 with each of its opt-in forms, the candidates for its default:
+
+- SILVANN_GFX950_DECODE_FUSED=1: the last split of each row and head block merges the others (no merge launch);
+- SILVANN_GFX950_DECODE_INLINE=1: each workgroup makes the plan itself at batches of at most 64 rows (no plan launch);
+- SILVANN_GFX950_DECODE_VTR=1: the V^T operand through the transposing LDS read at head_dim <= 256.
+
+A switch is read once a process, so the whole decode suite (tests/test_gpu_decode.py: the oracle, the torch fp32
+reference, zero-length rows, the closed forms, page-table bit-exactness, determinism) runs again in a child process
+with it on.
+"""
+import os
+import subprocess
+import sys
+from pathlib import Path
+
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+HERE = Path(__file__).resolve().parent
+
+
+@pytest.mark.timeout(400)
+@pytest.mark.parametrize("switch", ["SILVANN_GFX950_DECODE_FUSED", "SILVANN_GFX950_DECODE_INLINE",
+                                    "SILVANN_GFX950_DECODE_VTR"])
+def test_decode_suite_with(dev, switch):
+    print(f"case: tests/test_gpu_decode.py with {switch}=1 (child process)", flush=True)
+    cmd = [sys.executable, "-u", "-m", "pytest", str(HERE / "test_gpu_decode.py"), "-m", "gpu", "-x", "-q",
+           "-p", "no:cacheprovider", "--timeout", "120", "--timeout-method", "thread"]
+    r = subprocess.run(cmd, cwd=str(HERE.parent), env={**os.environ, switch: "1"},
+                       capture_output=True, text=True, timeout=360)
+    print(r.stdout[-4000:], r.stderr[-2000:], flush=True)
+    assert r.returncode == 0
