@@ -17,7 +17,8 @@
 #include <string.h>
 #include <unistd.h>
 
-#include <vector>
+#include <memory>
+#include <new>
 
 #include "../common.hpp"
 #include "../../../include/silvann_gfx950_attention.h"
@@ -131,27 +132,35 @@ bool memory_register_host(void* at, size_t bytes, void** card_at) {
     return false;
 }
 void memory_unregister_host(void* at) { (void)at; }
+// A handle is the descriptor plus one, so 0 is never a file (file.cuh:25-38's convention).
 bool file_open(const char* path, uint64_t* handle) {
-    const int fd = path ? open(path, O_RDONLY | O_CLOEXEC) : -1;
+    if (!path || !handle) return false;
+    const int fd = open(path, O_RDONLY | O_CLOEXEC);
     if (fd < 0) return false;
-    *handle = (uint64_t)fd;
+    *handle = (uint64_t)(uint32_t)fd + 1u;
     return true;
 }
-void file_close(uint64_t handle) { (void)close((int)handle); }
-// `bytes` of the file from `offset` into card memory at `to`, through a bounce buffer of up to 64 MiB
+void file_close(uint64_t handle) {
+    if (handle != 0) (void)close((int)(handle - 1));
+}
+// `bytes` of the file from `offset` into card memory at `to`, through a host bounce buffer of up to 64 MiB, each
+// piece written as memory_write writes (after the work queued before it); false on a short file or a failed copy
+// (file.cuh:89-102's contract)
 bool file_read(uint64_t handle, uint64_t offset, uint64_t bytes, void* to) {
-    flush_deferred();
+    if (handle == 0 || (!to && bytes != 0)) return false;
+    const int fd = (int)(handle - 1);
     const uint64_t piece = bytes < (64ull << 20) ? bytes : (64ull << 20);
-    std::vector<char> bounce(piece ? piece : 1);
+    std::unique_ptr<char[]> bounce(piece ? new (std::nothrow) char[piece] : nullptr);
+    if (piece && !bounce) return false;
     for (uint64_t done = 0; done < bytes;) {
         const uint64_t want = bytes - done < piece ? bytes - done : piece;
         uint64_t got = 0;
         while (got < want) {
-            const ssize_t n = pread((int)handle, bounce.data() + got, want - got, (off_t)(offset + done + got));
+            const ssize_t n = pread(fd, bounce.get() + got, want - got, (off_t)(offset + done + got));
             if (n <= 0) return false;
             got += (uint64_t)n;
         }
-        if (hipMemcpy((char*)to + done, bounce.data(), want, hipMemcpyHostToDevice) != hipSuccess) return false;
+        if (!memory_write((char*)to + done, bounce.get(), want)) return false;
         done += want;
     }
     return true;

@@ -111,8 +111,13 @@ def test_card_free_sys_doors(family, tmp_path):
     handle = ctypes.c_uint64()
     assert opened(str(tmp_path / "absent").encode(), ctypes.byref(handle)) is False
     (tmp_path / "there").write_bytes(b"x" * 10)
+    assert opened(None, ctypes.byref(handle)) is False
     assert opened(str(tmp_path / "there").encode(), ctypes.byref(handle)) is True
+    assert handle.value != 0   # 0 is never a file
     fn("file_close", None, ctypes.c_uint64)(handle.value)
+    fn("file_close", None, ctypes.c_uint64)(0)   # closes nothing
+    read = fn("file_read", ctypes.c_bool, ctypes.c_uint64, ctypes.c_uint64, ctypes.c_uint64, ctypes.c_void_p)
+    assert read(0, 0, 16, ctypes.addressof(buf)) is False   # no file: refused before any copy
     import torch
     if not torch.cuda.is_available():
         assert fn("device_count", ctypes.c_uint32)() == 0
