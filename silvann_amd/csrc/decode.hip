@@ -70,6 +70,10 @@ struct DecodeArgs {
     uint32_t* done;
     uint16_t* o;
     unsigned int* over;
+    // the inline plan with lens null: row u's length is len_first + u·len_step, and workgroup 0 writes the lengths
+    // to lens_out for the merge
+    uint32_t len_first, len_step;
+    uint32_t* lens_out;
 };
 
 // The scratch: the work counter, the plan, the finished-split counts (rows · kv heads · head blocks), then the
@@ -185,7 +189,12 @@ void decode_split(DecodeArgs a) {
     // split index — so no plan launch goes first.
     uint32_t lane_len = 0, lane_before = 0, inline_total = 0;
     if constexpr (INLINE) {
-        lane_len = lane < (int)a.rows ? a.lens[lane] : 0u;
+        if (a.lens) {
+            lane_len = lane < (int)a.rows ? a.lens[lane] : 0u;
+        } else {
+            lane_len = lane < (int)a.rows ? a.len_first + (uint32_t)lane * a.len_step : 0u;
+            if (blockIdx.x == 0 && w == 0 && lane < (int)a.rows) a.lens_out[lane] = lane_len;
+        }
         const uint32_t n = (lane_len + a.chunk - 1) / a.chunk;
         uint32_t incl = n, sum = n;
 #pragma unroll
@@ -636,6 +645,34 @@ bool vtr() {
     return on;
 }
 
+// The plan made inside decode_split at batches of at most 64 rows (SILVANN_GFX950_DECODE_INLINE=1): checked in the
+// CPU emulation, not yet measured on a GPU.
+bool inline_plan() {
+    static const bool on = [] {
+        const char* e = getenv("SILVANN_GFX950_DECODE_INLINE");
+        return e && strtol(e, nullptr, 10) > 0;
+    }();
+    return on;
+}
+
+// decode_split over contiguous caches, one workgroup an item, `splits` = rows · splits a row: head_dim 64-512, the
+// keys-are-values form at 512 when `shared`; INL makes the plan inside the kernel.
+template <bool INL>
+void split_contiguous(const DecodeArgs& a, uint64_t head_dim, bool shared, uint64_t splits, hipStream_t st) {
+    const uint64_t gh = (uint64_t)a.kv_heads * a.hblocks;
+    const dim3 grid((uint32_t)(splits * gh));
+    if (head_dim == 512) {
+        if (shared) decode_split<512, 2, false, false, true, false, true, INL><<<dim3(shared_grid(splits, gh)), kThreads, 0, st>>>(a);
+        else decode_split<512, 2, false, false, false, false, true, INL><<<grid, kThreads, 0, st>>>(a);
+    } else if (head_dim == 256) {
+        decode_split<256, kDefaultVariant, false, false, false, false, false, INL><<<grid, kThreads, 0, st>>>(a);
+    } else if (head_dim == 128) {
+        decode_split<128, kDefaultVariant, false, false, false, false, false, INL><<<grid, kThreads, 0, st>>>(a);
+    } else {
+        decode_split<64, kDefaultVariant, false, false, false, false, false, INL><<<grid, kThreads, 0, st>>>(a);
+    }
+}
+
 uint32_t head_blocks(uint64_t q_heads, uint64_t kv_heads) { return (uint32_t)((q_heads / kv_heads + 15) / 16); }
 
 bool decode_shape_ok(uint64_t q_heads, uint64_t kv_heads, uint64_t head_dim, uint64_t most, uint64_t rows) {
@@ -672,6 +709,8 @@ void decode_paged_launch(uint16_t* o, const uint16_t* q, const uint16_t* k, cons
     a.rows = (uint32_t)rows;
     a.o = o;
     a.over = over;
+    a.len_first = a.len_step = 0;
+    a.lens_out = nullptr;
     const dim3 mgrid((uint32_t)q_heads, (uint32_t)rows, (uint32_t)(head_dim / 64));
     hipStream_t st = stream();
     static const int variant = [] {
@@ -719,13 +758,8 @@ void decode_paged_launch(uint16_t* o, const uint16_t* q, const uint16_t* k, cons
         check_launch("attention_decode_paged");
         return;
     }
-    // the plan made inside decode_split (SILVANN_GFX950_DECODE_INLINE=1, batches of at most 64 rows): one launch
-    // fewer a step; checked in the CPU emulation, not yet measured on a GPU
-    static const bool inline_plan = [] {
-        const char* e = getenv("SILVANN_GFX950_DECODE_INLINE");
-        return e && strtol(e, nullptr, 10) > 0;
-    }();
-    const bool inlined = inline_plan && rows <= 64 && head_dim <= 256 && !persistent && !vtr();
+    // the plan made inside decode_split at batches of at most 64 rows: one launch fewer a step
+    const bool inlined = inline_plan() && rows <= 64 && head_dim <= 256 && !persistent && !vtr();
     if (!inlined) decode_plan<<<1, 256, 0, st>>>(lens, a.rows, a.chunk, (uint32_t*)a.plan, a.counter);
     prof_begin(kProfDecodeSplit);
     // head_dim 512: one workgroup an item; the shared-tile form when the keys are the values
@@ -831,19 +865,18 @@ bool decode_one(uint16_t* o, float* res, const uint16_t* q, const uint16_t* k, c
     a.rows = 1;
     a.o = o;
     a.over = over;
+    a.len_first = a.len_step = 0;
+    a.lens_out = nullptr;
     hipStream_t st = stream();
-    decode_plan_one<<<1, 64, 0, st>>>(lens, (uint32_t)length, (uint32_t)nsplit, (uint32_t*)a.plan, a.counter);
-    const dim3 grid((uint32_t)(nsplit * kv_heads * hblocks));
     prof_begin(kProfDecodeSplit);
-    if (head_dim == 512) {
-        if (k == v) decode_split<512, 2, false, false, true><<<dim3(shared_grid(nsplit, kv_heads * hblocks)), kThreads, 0, st>>>(a);
-        else decode_split<512, 2, false, false><<<grid, kThreads, 0, st>>>(a);
-    } else if (head_dim == 256) {
-        decode_split<256, kDefaultVariant, false, false><<<grid, kThreads, 0, st>>>(a);
-    } else if (head_dim == 128) {
-        decode_split<128, kDefaultVariant, false, false><<<grid, kThreads, 0, st>>>(a);
+    if (inline_plan()) {   // the length from the host, written out for the merge by the split kernel
+        a.lens = nullptr;
+        a.len_first = (uint32_t)length;
+        a.lens_out = lens;
+        split_contiguous<true>(a, head_dim, k == v, nsplit, st);
     } else {
-        decode_split<64, kDefaultVariant, false, false><<<grid, kThreads, 0, st>>>(a);
+        decode_plan_one<<<1, 64, 0, st>>>(lens, (uint32_t)length, (uint32_t)nsplit, (uint32_t*)a.plan, a.counter);
+        split_contiguous<false>(a, head_dim, k == v, nsplit, st);
     }
     prof_end(kProfDecodeSplit);
     const dim3 mgrid((uint32_t)q_heads, 1, (uint32_t)(head_dim / 64));
@@ -909,21 +942,20 @@ bool decode_causal(uint16_t* o, const uint16_t* q, const uint16_t* k, const uint
     a.rows = (uint32_t)rows;
     a.o = o;
     a.over = over;
+    a.len_first = a.len_step = 0;
+    a.lens_out = nullptr;
     hipStream_t st = stream();
-    causal_lens<<<(uint32_t)((rows + 255) / 256), 256, 0, st>>>(lens, (uint32_t)first, (uint32_t)rows);
-    decode_plan<<<1, 256, 0, st>>>(lens, a.rows, a.chunk, (uint32_t*)a.plan, a.counter);
-    const dim3 grid((uint32_t)(rows * a.nsplit * kv_heads * hblocks));
     prof_begin(kProfDecodeSplit);
-    if (head_dim == 512) {
-        if (k == v)
-            decode_split<512, 2, false, false, true><<<dim3(shared_grid(rows * a.nsplit, kv_heads * hblocks)), kThreads, 0, st>>>(a);
-        else decode_split<512, 2, false, false><<<grid, kThreads, 0, st>>>(a);
-    } else if (head_dim == 256) {
-        decode_split<256, kDefaultVariant, false, false><<<grid, kThreads, 0, st>>>(a);
-    } else if (head_dim == 128) {
-        decode_split<128, kDefaultVariant, false, false><<<grid, kThreads, 0, st>>>(a);
+    if (inline_plan() && rows <= 64) {   // row u's length first + u + 1, written out for the merge by the split kernel
+        a.lens = nullptr;
+        a.len_first = (uint32_t)first + 1u;
+        a.len_step = 1;
+        a.lens_out = lens;
+        split_contiguous<true>(a, head_dim, k == v, rows * a.nsplit, st);
     } else {
-        decode_split<64, kDefaultVariant, false, false><<<grid, kThreads, 0, st>>>(a);
+        causal_lens<<<(uint32_t)((rows + 255) / 256), 256, 0, st>>>(lens, (uint32_t)first, (uint32_t)rows);
+        decode_plan<<<1, 256, 0, st>>>(lens, a.rows, a.chunk, (uint32_t*)a.plan, a.counter);
+        split_contiguous<false>(a, head_dim, k == v, rows * a.nsplit, st);
     }
     prof_end(kProfDecodeSplit);
     const dim3 mgrid((uint32_t)q_heads, (uint32_t)rows, (uint32_t)(head_dim / 64));
@@ -974,20 +1006,15 @@ bool decode_rows_fit(uint16_t* o, const uint16_t* q, const uint16_t* k, const ui
     a.rows = (uint32_t)rows;
     a.o = o;
     a.over = over;
+    a.len_first = a.len_step = 0;
+    a.lens_out = nullptr;
     hipStream_t st = stream();
-    decode_plan<<<1, 256, 0, st>>>(lens, a.rows, a.chunk, (uint32_t*)a.plan, a.counter);
-    const dim3 grid((uint32_t)(rows * a.nsplit * kv_heads * hblocks));
     prof_begin(kProfDecodeSplit);
-    if (head_dim == 512) {
-        if (k == v)
-            decode_split<512, 2, false, false, true><<<dim3(shared_grid(rows * a.nsplit, kv_heads * hblocks)), kThreads, 0, st>>>(a);
-        else decode_split<512, 2, false, false><<<grid, kThreads, 0, st>>>(a);
-    } else if (head_dim == 256) {
-        decode_split<256, kDefaultVariant, false, false><<<grid, kThreads, 0, st>>>(a);
-    } else if (head_dim == 128) {
-        decode_split<128, kDefaultVariant, false, false><<<grid, kThreads, 0, st>>>(a);
+    if (inline_plan() && rows <= 64) {
+        split_contiguous<true>(a, head_dim, k == v, rows * a.nsplit, st);
     } else {
-        decode_split<64, kDefaultVariant, false, false><<<grid, kThreads, 0, st>>>(a);
+        decode_plan<<<1, 256, 0, st>>>(lens, a.rows, a.chunk, (uint32_t*)a.plan, a.counter);
+        split_contiguous<false>(a, head_dim, k == v, rows * a.nsplit, st);
     }
     prof_end(kProfDecodeSplit);
     const dim3 mgrid((uint32_t)q_heads, (uint32_t)rows, (uint32_t)(head_dim / 64));

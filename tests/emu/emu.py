@@ -162,13 +162,14 @@ def run_rope_rows(x, cs, rows, heads, head_stride, row_stride, rot, timeout: int
     return _run({"q": x, "k": cs}, params, None, timeout, outs=(("o", np.uint16),))
 
 
-def run_chain(kind, q, k, v, qh, kvh, hd, a0, a1=0, interleave=False, defer=True, timeout: int = 900):
+def run_chain(kind, q, k, v, qh, kvh, hd, a0, a1=0, interleave=False, defer=True, timeout: int = 900,
+              extra_env: dict | None = None):
     """A reference verb's door chain through the library's doors: kind "decode" (scores, mix; a0 = length),
     "weights" (weights, residual_mix; a0 = length) or "causal" (causal_scores_grouped, causal_softmax, causal_mix;
     a0 = first, a1 = rows). `interleave` puts another door inside the chain; `defer` False runs every door on its
-    own. Answers the fp16 answers, the weights buffer afterwards, the residual (not for "causal") and the fault
-    word."""
-    env = None if defer else {"SILVANN_GFX950_DEFER": "0"}
+    own; `extra_env` adds switches. Answers the fp16 answers, the weights buffer afterwards, the residual (not for
+    "causal"), the fault word and the emulation's log."""
+    env = {**({} if defer else {"SILVANN_GFX950_DEFER": "0"}), **(extra_env or {})} or None
     if kind == "causal":
         params = f"chain_causal {qh} {kvh} {hd} {a0} {a1} {1 if interleave else 0} 0 0"
         return _run({"q": q, "k": k, "v": v}, params, env, timeout, outs=(("o", np.float16), ("p", np.float32)))
@@ -190,7 +191,8 @@ def run_chain_residual(kind, q, kcodes, kscales, vcodes, vscales, qh, kvh, hd, a
     return _run(files, params, env, timeout, outs=(("p", np.float32), ("res", np.float32)))
 
 
-def run_chain_grouped(q, k, v, qh, kvh, hd, length, sink=None, interleave=False, timeout: int = 900):
+def run_chain_grouped(q, k, v, qh, kvh, hd, length, sink=None, interleave=False, timeout: int = 900,
+                      extra_env: dict | None = None):
     """Latent attention's chain as GLM and DeepSeek call it: attention_scores_grouped, then attention_softmax_rows
     (sink None) or attention_softmax_sink, then attention_mix. `v` None: the keys are the values. The answers, the
     weights buffer afterwards and the fault word."""
@@ -198,13 +200,14 @@ def run_chain_grouped(q, k, v, qh, kvh, hd, length, sink=None, interleave=False,
     files = {"q": q, "k": k, "v": v}
     if sink is not None:
         files["lens"] = np.ascontiguousarray(sink, np.uint16)
-    return _run(files, params, None, timeout, outs=(("o", np.float16), ("p", np.float32)))
+    return _run(files, params, extra_env, timeout, outs=(("o", np.float16), ("p", np.float32)))
 
 
-def run_chain_grouped_rows(q, lat, lens, qh, hd, most, interleave=False, timeout: int = 900):
+def run_chain_grouped_rows(q, lat, lens, qh, hd, most, interleave=False, timeout: int = 900,
+                           extra_env: dict | None = None):
     """GLM's block chain: attention_scores_grouped_rows, attention_softmax_lens, attention_mix_rows, one kv head, row u
     over its own `lens[u]` latents at lat + u·most·hd (keys and values). The answers, the weights buffer afterwards
     and the fault word."""
     params = f"chain_grows {qh} 1 {hd} {most} {len(lens)} {1 if interleave else 0} 0 {most * hd}"
-    return _run({"q": q, "k": lat, "lens": np.ascontiguousarray(lens, np.uint32)}, params, None, timeout,
+    return _run({"q": q, "k": lat, "lens": np.ascontiguousarray(lens, np.uint32)}, params, extra_env, timeout,
                 outs=(("o", np.float16), ("p", np.float32)))

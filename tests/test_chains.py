@@ -177,3 +177,70 @@ def test_grouped_rows_chain(oracle, interleave, fused):
         assert not np.allclose(p[valid], wp[valid], rtol=1e-4, atol=1e-6)
     else:
         np.testing.assert_allclose(p[valid], wp[valid], rtol=1e-4, atol=1e-6)
+
+
+INLINE = {"SILVANN_GFX950_DECODE_INLINE": "1", "EMU_LAUNCHES": "1"}
+PLANS = ("decode_plan", "causal_lens")   # decode_plan_one too
+
+
+def _launched(log):
+    return [ln[len("emu launch "):] for ln in log.splitlines() if ln.startswith("emu launch ")]
+
+
+@pytest.mark.parametrize("kind,qh,kvh,hd,a0,a1,shared", [
+    ("decode", 16, 2, 256, 2048, 0, False),   # the decode verb's pair, one query of a host length
+    ("decode", 32, 1, 512, 600, 0, False),    # head_dim 512, two head blocks
+    ("weights", 16, 2, 128, 3000, 0, False),  # the residual pair: the merge writes the residual
+    ("causal", 8, 1, 512, 530, 3, False),     # head_dim 512 rows: lengths first + u + 1 made in the kernel
+    ("causal", 20, 1, 512, 530, 2, True),     # latent block prefill, keys = values
+])
+def test_chains_with_inline_plan(oracle, kind, qh, kvh, hd, a0, a1, shared):
+    """The fused decode routes with the plan made inside decode_split (SILVANN_GFX950_DECODE_INLINE=1): the same
+    answers, and no plan or length kernel launched (the emulation's launch log)."""
+    rows = a1 or 1
+    n = a0 + a1 if kind == "causal" else a0
+    q, k, v = _inputs(qh + hd + n + 1, qh, kvh, hd, n, rows)
+    if shared:
+        v = k
+    if kind == "causal":
+        o, p, over, log = emu.run_chain("causal", q, k, None if shared else v, qh, kvh, hd, a0, a1,
+                                        extra_env=INLINE)
+        want, _ = oracle.causal_rows(q, k, v, None, 0, qh, kvh, hd, a0, list(range(a1)))
+        parity(o, want)
+    else:
+        o, p, res, over, log = emu.run_chain(kind, q, k, v, qh, kvh, hd, a0, extra_env=INLINE)
+        if kind == "decode":
+            want_o, _ = oracle.mix(oracle.scores(q, k, qh, kvh, hd, a0), v, qh, kvh, hd, a0)
+            parity(o, want_o)
+        else:
+            wp, wres = oracle.weights(q, k, qh, kvh, hd, a0)
+            residual_parity(res, oracle.residual_mix(wres, wp, v, qh, kvh, hd, a0), hd)
+    assert over == 0
+    launched = _launched(log)
+    assert any("decode_split" in x for x in launched), launched
+    assert not [x for x in launched if x.startswith(PLANS)], launched
+
+
+def test_latent_chains_with_inline_plan(oracle):
+    """Latent attention's decode chain (scores_grouped, softmax_sink, mix) and block chain (scores_grouped_rows,
+    softmax_lens, mix_rows) with the plan made inside decode_split."""
+    qh, hd, length = 16, 512, 1100
+    rng = np.random.default_rng(5)
+    q = rng.standard_normal(qh * hd).astype(np.float16)
+    lat = rng.standard_normal(length * hd).astype(np.float16)
+    s = (rng.standard_normal(qh) * 2 + 1).astype(np.float16).view(np.uint16)
+    o, _, over, log = emu.run_chain_grouped(q, lat, None, qh, 1, hd, length, sink=s, extra_env=INLINE)
+    wp = oracle.softmax_sink(oracle.scores_grouped(q, lat, qh, 1, hd, length), s, qh, length)
+    parity(o, oracle.mix(wp, lat, qh, 1, hd, length)[0])
+    assert over == 0 and not [x for x in _launched(log) if x.startswith(PLANS)]
+
+    lens = np.asarray([1100, 1, 700], np.uint32)
+    most, rows = int(lens.max()), len(lens)
+    q = rng.standard_normal(rows * qh * hd).astype(np.float16)
+    lat = rng.standard_normal(rows * most * hd).astype(np.float16)
+    o, _, over, log = emu.run_chain_grouped_rows(q, lat, lens, qh, hd, most, extra_env=INLINE)
+    p_row = qh * most
+    raw = oracle.scores_grouped_rows(p_row, q, qh * hd, lat, most * hd, lens, qh, 1, hd, most, rows)
+    wp = oracle.softmax_lens(raw, p_row, lens, qh, rows)
+    parity(o, oracle.mix_rows(qh * hd, wp, p_row, lat, most * hd, lens, qh, 1, hd, rows)[0])
+    assert over == 0 and not [x for x in _launched(log) if x.startswith(PLANS)]

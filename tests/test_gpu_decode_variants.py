@@ -6,7 +6,7 @@
 
 A switch is read once a process, so the whole decode suite (tests/test_gpu_decode.py: the oracle, the torch fp32
 reference, zero-length rows, the closed forms, page-table bit-exactness, determinism) runs again in a child process
-with it on.
+with it on — and with the inline plan, which the deferred chains' fused routes take too, the chain and latent suites.
 """
 import os
 import subprocess
@@ -20,12 +20,18 @@ pytestmark = pytest.mark.gpu
 HERE = Path(__file__).resolve().parent
 
 
+SUITES = {
+    "SILVANN_GFX950_DECODE_FUSED": ["test_gpu_decode.py"],
+    "SILVANN_GFX950_DECODE_INLINE": ["test_gpu_decode.py", "test_gpu_chains.py", "test_gpu_latent.py"],
+    "SILVANN_GFX950_DECODE_VTR": ["test_gpu_decode.py"],
+}
+
+
 @pytest.mark.timeout(400)
-@pytest.mark.parametrize("switch", ["SILVANN_GFX950_DECODE_FUSED", "SILVANN_GFX950_DECODE_INLINE",
-                                    "SILVANN_GFX950_DECODE_VTR"])
+@pytest.mark.parametrize("switch", list(SUITES))
 def test_decode_suite_with(dev, switch):
-    print(f"case: tests/test_gpu_decode.py with {switch}=1 (child process)", flush=True)
-    cmd = [sys.executable, "-u", "-m", "pytest", str(HERE / "test_gpu_decode.py"), "-m", "gpu", "-x", "-q",
+    print(f"case: {' '.join(SUITES[switch])} with {switch}=1 (child process)", flush=True)
+    cmd = [sys.executable, "-u", "-m", "pytest", *[str(HERE / f) for f in SUITES[switch]], "-m", "gpu", "-x", "-q",
            "-p", "no:cacheprovider", "--timeout", "120", "--timeout-method", "thread"]
     r = subprocess.run(cmd, cwd=str(HERE.parent), env={**os.environ, switch: "1"},
                        capture_output=True, text=True, timeout=360)
