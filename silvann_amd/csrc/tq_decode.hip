@@ -33,6 +33,8 @@ namespace {
 constexpr int kWaves = 4;
 constexpr int kThreads = 64 * kWaves;
 constexpr uint32_t kMaxSplits = 65536;
+// Workgroups one launch of tq_split may have: its item index and the grid's thread count stay 32-bit.
+constexpr uint64_t kMaxGroups = (1ull << 32) / kThreads - 1;
 
 struct TqArgs {
     const uint16_t* q;
@@ -337,8 +339,12 @@ void residual_tq_launch(float* res, const uint16_t* q, const uint8_t* kc, const 
         refuse("attention_residual_tq");
         return;
     }
-    residual_tq_run(res, q, kc, ks, vc, vs, q_heads, kv_heads, head_dim, length, d, rows, scratch,
-                    tq_chunk(head_dim, kv_heads, tq_hblocks(q_heads, kv_heads), length, rows));
+    const uint32_t chunk = tq_chunk(head_dim, kv_heads, tq_hblocks(q_heads, kv_heads), length, rows);
+    if ((length + chunk - 1) / chunk * kv_heads * tq_hblocks(q_heads, kv_heads) * rows > kMaxGroups) {
+        refuse("attention_residual_tq");
+        return;
+    }
+    residual_tq_run(res, q, kc, ks, vc, vs, q_heads, kv_heads, head_dim, length, d, rows, scratch, chunk);
 }
 
 // The deferred TurboQuant pairs' fused form: weights_tq(_rows) + residual_mix_tq(_rows) as row 139, its scratch the
@@ -358,7 +364,7 @@ bool residual_tq_fit(float* res, const uint16_t* q, const uint8_t* kc, const uin
     uint64_t chunk = tq_chunk(head_dim, kv_heads, hb, length, rows);
     if ((length + chunk - 1) / chunk > fit) chunk = ((length + fit - 1) / fit + step - 1) / step * step;
     const uint64_t nsplit = (length + chunk - 1) / chunk;
-    if (nsplit > fit || nsplit > kMaxSplits) return false;
+    if (nsplit > fit || nsplit > kMaxSplits || nsplit * kv_heads * hb * rows > kMaxGroups) return false;
     residual_tq_run(res, q, kc, ks, vc, vs, q_heads, kv_heads, head_dim, length, d, rows, (float*)scratch,
                     (uint32_t)chunk);
     return true;
