@@ -22,7 +22,8 @@ latent attention (64 heads over 131,072 512-wide latents, row 137 with k = v) in
 The TurboQuant, writer and latent lines run as child processes (`--only 6`..`9`), each under a time limit, so a
 failure there is recorded in its entry and cannot take the headline down; so does C2 once more with the split-K
 decode's opt-in candidates for its default (the fused finish, SILVANN_GFX950_DECODE_FUSED=1; the transposing V^T
-reads, SILVANN_GFX950_DECODE_VTR=1; the plan made inside decode_split, SILVANN_GFX950_DECODE_INLINE=1), and C5 / C3 through the
+reads, SILVANN_GFX950_DECODE_VTR=1; the plan made inside decode_split, SILVANN_GFX950_DECODE_INLINE=1; the last two
+together, one launch a step), and C5 / C3 through the
 reference's own decode and rows verbs, whose door chains this library defers and runs fused.
 
 `cpu_baseline` is the reference's own x86_avx2 silicon family (oracle/_ref, built from the reference's
@@ -434,6 +435,9 @@ def main():
                                   variant="transposing V^T reads"))
         secondary.append(isolated(2, a.steps, a.warmup, env={"SILVANN_GFX950_DECODE_INLINE": "1"},
                                   variant="plan inside decode_split (no plan launch)"))
+        secondary.append(isolated(2, a.steps, a.warmup,
+                                  env={"SILVANN_GFX950_DECODE_INLINE": "1", "SILVANN_GFX950_DECODE_FUSED": "1"},
+                                  variant="one launch a step (inline plan + fused finish)"))
         for n in (10, 11):
             secondary.append(isolated(n, max(5, a.steps // 2), a.warmup))
     cpu = None if a.no_cpu else cpu_baseline(w2, a.cpu_threads)

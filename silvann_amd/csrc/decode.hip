@@ -37,6 +37,8 @@
 //                    residual, decode_merge<…, SINK> folds the sink in
 //   decode_causal    a deferred causal chain at head_dim 512: each row a decode over the same cache
 #include <math.h>
+#include <atomic>
+#include <random>
 #include <stdio.h>
 #include <stdlib.h>
 
@@ -74,13 +76,19 @@ struct DecodeArgs {
     // to lens_out for the merge
     uint32_t len_first, len_step;
     uint32_t* lens_out;
+    uint64_t tag;   // the fused finish with the inline plan: this call's tag for the counts (below kTagMask)
 };
 
-// The scratch: the work counter, the plan, the finished-split counts (rows · kv heads · head blocks), then the
-// partial residuals [row][q head][split][head_dim + 2].
+// The scratch: the work counter, the plan, the finished-split counts (rows · kv heads · head blocks, 8 bytes each:
+// 32-bit counts, or the inline plan's tagged 64-bit words), then the partial residuals
+// [row][q head][split][head_dim + 2].
 constexpr uint64_t kPlanAt = 64;
-uint64_t done_at(uint64_t rows) { return kPlanAt + 4 * (rows + 1); }
-uint64_t part_at(uint64_t rows, uint64_t units) { return (done_at(rows) + 4 * rows * units + 255) / 256 * 256; }
+uint64_t done_at(uint64_t rows) { return (kPlanAt + 4 * (rows + 1) + 7) / 8 * 8; }
+uint64_t part_at(uint64_t rows, uint64_t units) { return (done_at(rows) + 8 * rows * units + 255) / 256 * 256; }
+// A tagged finished-split count: the call's tag in the top 40 bits, the count below. A word holding another tag
+// (an earlier call's, or whatever the scratch held) counts as zero, so no launch has to clear the counts first.
+constexpr int kTagShift = 24;
+constexpr uint64_t kTagMask = (1ull << (64 - kTagShift)) - 1;
 // A launch's work-items (workgroups × 256) must stay below 2^32: the most workgroups a split grid may have.
 constexpr uint64_t kMaxGroups = (1ull << 32) / kThreads - 8;
 
@@ -168,7 +176,8 @@ template <int HD, int VARIANT, bool GROUPED, bool PERSISTENT, bool SHARED = fals
           bool INLINE = false>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(HD >= 512 ? 1 : 2, HD >= 512 ? 1 : 2)))
 void decode_split(DecodeArgs a) {
-    static_assert(!INLINE || (!PERSISTENT && !FUSED), "the inline plan is for one workgroup an item, merged apart");
+    static_assert(!INLINE || !PERSISTENT, "the inline plan is for one workgroup an item");
+    static_assert(!(FUSED && INLINE) || kMaxSplits < (1u << kTagShift), "a tagged count holds every split");
     constexpr int TK = tile_keys(HD);  // keys a wave takes a step: 32 KB of K and V whatever the head width
     constexpr int MT = TK / 16;      // 16-key M tiles of S^T
     constexpr int KS = HD / 32;      // k-steps of the S^T MFMA (32 dims each)
@@ -205,6 +214,18 @@ void decode_split(DecodeArgs a) {
         }
         lane_before = incl - n;
         inline_total = __builtin_amdgcn_readfirstlane(sum) * GH;
+        if constexpr (FUSED) {
+            // rows with no positions have no split to finish them: workgroup 0 writes their zero answers
+            if (blockIdx.x == 0) {
+                uint64_t empty = __builtin_amdgcn_ballot_w64(lane < (int)a.rows && lane_len == 0);
+                const uint32_t halves = a.q_heads * HD;
+                while (empty) {
+                    const uint32_t e = (uint32_t)__builtin_ctzll(empty);
+                    empty &= empty - 1;
+                    for (uint32_t i = threadIdx.x; i < halves; i += kThreads) a.o[(uint64_t)e * halves + i] = 0;
+                }
+            }
+        }
     }
     const uint32_t total = INLINE ? inline_total : a.plan[a.rows] * GH;
     __shared__ uint32_t item_at;
@@ -423,7 +444,22 @@ void decode_split(DecodeArgs a) {
         __threadfence();
         __syncthreads();
         const uint32_t ns = (len + a.chunk - 1) / a.chunk;
-        if (threadIdx.x == 0) is_last = atomicAdd(a.done + (uint64_t)u * GH + gh, 1u) == ns - 1;
+        if (threadIdx.x == 0) {
+            if constexpr (INLINE) {
+                // no plan launch cleared the count: a word of another tag is a count of zero
+                unsigned long long* word = (unsigned long long*)a.done + (uint64_t)u * GH + gh;
+                unsigned long long seen = *(volatile unsigned long long*)word, was;   // a guess the CAS corrects
+                uint32_t count;
+                do {
+                    was = seen;
+                    count = (was >> kTagShift) == a.tag ? (uint32_t)(was & ((1u << kTagShift) - 1)) : 0u;
+                    seen = atomicCAS(word, was, (a.tag << kTagShift) | (count + 1u));
+                } while (seen != was);
+                is_last = count == ns - 1;
+            } else {
+                is_last = atomicAdd(a.done + (uint64_t)u * GH + gh, 1u) == ns - 1;
+            }
+        }
         __syncthreads();
         if (is_last) {
             __threadfence();
@@ -645,6 +681,16 @@ bool vtr() {
     return on;
 }
 
+// This call's tag for the fused finish's tagged counts: a process-wide serial from a random start, 40 bits, so a
+// count word left by another call (or any earlier contents of the scratch) shows another tag but by a 2^-40 chance.
+uint64_t next_tag() {
+    static std::atomic<uint64_t> serial{[] {
+        std::random_device rd;
+        return ((uint64_t)rd() << 32) ^ (uint64_t)rd();
+    }()};
+    return serial.fetch_add(1, std::memory_order_relaxed) & kTagMask;
+}
+
 // The plan made inside decode_split at batches of at most 64 rows (SILVANN_GFX950_DECODE_INLINE=1): checked in the
 // CPU emulation, not yet measured on a GPU.
 bool inline_plan() {
@@ -711,6 +757,7 @@ void decode_paged_launch(uint16_t* o, const uint16_t* q, const uint16_t* k, cons
     a.over = over;
     a.len_first = a.len_step = 0;
     a.lens_out = nullptr;
+    a.tag = 0;
     const dim3 mgrid((uint32_t)q_heads, (uint32_t)rows, (uint32_t)(head_dim / 64));
     hipStream_t st = stream();
     static const int variant = [] {
@@ -739,6 +786,24 @@ void decode_paged_launch(uint16_t* o, const uint16_t* q, const uint16_t* k, cons
         const char* e = getenv("SILVANN_GFX950_DECODE_FUSED");
         return e && strtol(e, nullptr, 10) > 0;
     }();
+    if (fused && head_dim <= 256 && !persistent && inline_plan() && rows <= 64) {
+        // one launch: the plan made in the kernel, the counts tagged with this call's tag
+        a.tag = next_tag();
+        prof_begin(kProfDecodeSplit);
+        const uint32_t hv = (uint32_t)head_dim;
+        if (grouped) {
+            if (hv == 64) decode_split<64, kDefaultVariant, true, false, false, true, false, true><<<igrid, kThreads, 0, st>>>(a);
+            else if (hv == 128) decode_split<128, kDefaultVariant, true, false, false, true, false, true><<<igrid, kThreads, 0, st>>>(a);
+            else decode_split<256, kDefaultVariant, true, false, false, true, false, true><<<igrid, kThreads, 0, st>>>(a);
+        } else {
+            if (hv == 64) decode_split<64, kDefaultVariant, false, false, false, true, false, true><<<igrid, kThreads, 0, st>>>(a);
+            else if (hv == 128) decode_split<128, kDefaultVariant, false, false, false, true, false, true><<<igrid, kThreads, 0, st>>>(a);
+            else decode_split<256, kDefaultVariant, false, false, false, true, false, true><<<igrid, kThreads, 0, st>>>(a);
+        }
+        prof_end(kProfDecodeSplit);
+        check_launch("attention_decode_paged");
+        return;
+    }
     if (fused && head_dim <= 256 && !persistent) {
         const uint32_t units = a.kv_heads * a.hblocks;
         decode_plan<true><<<1, 256, 0, st>>>(lens, a.rows, a.chunk, (uint32_t*)a.plan, a.counter, a.done, units, o,
@@ -867,6 +932,7 @@ bool decode_one(uint16_t* o, float* res, const uint16_t* q, const uint16_t* k, c
     a.over = over;
     a.len_first = a.len_step = 0;
     a.lens_out = nullptr;
+    a.tag = 0;
     hipStream_t st = stream();
     prof_begin(kProfDecodeSplit);
     if (inline_plan()) {   // the length from the host, written out for the merge by the split kernel
@@ -944,6 +1010,7 @@ bool decode_causal(uint16_t* o, const uint16_t* q, const uint16_t* k, const uint
     a.over = over;
     a.len_first = a.len_step = 0;
     a.lens_out = nullptr;
+    a.tag = 0;
     hipStream_t st = stream();
     prof_begin(kProfDecodeSplit);
     if (inline_plan() && rows <= 64) {   // row u's length first + u + 1, written out for the merge by the split kernel
@@ -1008,6 +1075,7 @@ bool decode_rows_fit(uint16_t* o, const uint16_t* q, const uint16_t* k, const ui
     a.over = over;
     a.len_first = a.len_step = 0;
     a.lens_out = nullptr;
+    a.tag = 0;
     hipStream_t st = stream();
     prof_begin(kProfDecodeSplit);
     if (inline_plan() && rows <= 64) {

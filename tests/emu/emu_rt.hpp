@@ -160,6 +160,10 @@ inline unsigned int atomicCAS(unsigned int* p, unsigned int cmp, unsigned int va
     __atomic_compare_exchange_n(p, &cmp, val, false, __ATOMIC_SEQ_CST, __ATOMIC_SEQ_CST);
     return cmp;
 }
+inline unsigned long long atomicCAS(unsigned long long* p, unsigned long long cmp, unsigned long long val) {
+    __atomic_compare_exchange_n(p, &cmp, val, false, __ATOMIC_SEQ_CST, __ATOMIC_SEQ_CST);
+    return cmp;
+}
 typedef int hipError_t;
 constexpr hipError_t hipSuccess = 0;
 enum { hipDeviceAttributeMultiprocessorCount = 0 };

@@ -3,6 +3,7 @@
 // wrote to a directory, and writes the answer back there. Every buffer sits against an inaccessible page, so an out-of-bounds read or write stops the
 // run with the buffer, the offset and the lane that made it; a run that outlives its time limit (a lost
 // barrier) stops too.
+#include <vector>
 #include <execinfo.h>
 #include <signal.h>
 #include <sys/mman.h>
@@ -365,9 +366,18 @@ int main(int argc, char** argv) {
         const uint64_t sb = silvann_gfx950_attention_decode_paged_scratch(qh, kvh, hd, a0, a1);
         float* scratch = (float*)guarded(sb ? sb : 4, "scratch");
         memset(scratch, 0xFF, sb ? sb : 4);   // whatever a caller's scratch held before
-        silvann_gfx950_attention_decode_paged((uint16_t*)o, (const uint16_t*)q, (const uint16_t*)k, (const uint16_t*)v,
-                                              (const uint32_t*)pages, pages_row, ps, k_row, (const uint32_t*)lens, qh, kvh,
-                                              hd, a0, a1, scratch, over);
+        // EMU_REPEAT: a first call with every query negated, then the call whose answers are kept, over the scratch
+        // the first left (its partials differ from the second's), the answers cleared between
+        const int calls = getenv("EMU_REPEAT") ? 2 : 1;
+        std::vector<uint16_t> decoy((const uint16_t*)q, (const uint16_t*)q + a1 * qh * hd);
+        for (uint16_t& h : decoy) h ^= 0x8000u;
+        for (int c = 0; c < calls; ++c) {
+            if (c) memset(o, 0xFF, on);
+            const uint16_t* qc = c + 1 < calls ? decoy.data() : (const uint16_t*)q;
+            silvann_gfx950_attention_decode_paged((uint16_t*)o, qc, (const uint16_t*)k, (const uint16_t*)v,
+                                                  (const uint32_t*)pages, pages_row, ps, k_row, (const uint32_t*)lens, qh,
+                                                  kvh, hd, a0, a1, scratch, over);
+        }
     }
     save(d + "/o.bin", o, on);
     save(d + "/over.bin", over, 4);

@@ -148,3 +148,25 @@ def test_decode_inline_plan(oracle, qh, kvh, hd, lens, ps):
     assert over == 0
     launched = [ln for ln in log.splitlines() if ln.startswith("emu launch ")]
     assert len(launched) == 2 and "decode_split" in launched[0] and "decode_merge" in launched[1], launched
+
+
+@pytest.mark.parametrize("qh,kvh,hd,lens,ps", [
+    (16, 2, 256, [700, 0, 2048, 0], 256),                  # empty rows: zero answers from workgroup 0
+    (8, 2, 128, [1, 17, 3000], 0),                         # a row of many splits beside one-split rows
+    (4, 4, 64, [(37 * i) % 300 for i in range(64)], 16),   # 64 rows, pages shorter than a tile
+])
+@pytest.mark.parametrize("repeat", [False, True])
+def test_decode_one_launch(oracle, qh, kvh, hd, lens, ps, repeat):
+    """Row 137 as one launch (SILVANN_GFX950_DECODE_FUSED=1 with SILVANN_GFX950_DECODE_INLINE=1): the plan made in the
+    kernel, the finish fused, its counts tagged with the call's tag over a scratch that starts as garbage — or, with
+    `repeat`, over the complete counts a first call left (counted again as zero: another tag) — the oracle's
+    answers, and only decode_split in the launch log."""
+    w = W.decode("emu", qh, kvh, hd, lens, page_size=ps, seed=hd + len(lens) + 13)
+    env = {**FUSED, **INLINE, **({"EMU_REPEAT": "1"} if repeat else {})}
+    got, over, log = emu.run_decode(w, env=env)
+    want, _ = oracle.decode_paged(w.q, w.k, w.v, w.pages, w.pages_row, w.page_size, w.k_row, w.lens, qh, kvh, hd,
+                                  w.rows)
+    parity(got, want)
+    assert over == 0
+    launched = [ln for ln in log.splitlines() if ln.startswith("emu launch ")]
+    assert len(launched) == 1 + repeat and all("decode_split" in x for x in launched), launched

@@ -2,6 +2,7 @@
 
 - SILVANN_GFX950_DECODE_FUSED=1: the last split of each row and head block merges the others (no merge launch);
 - SILVANN_GFX950_DECODE_INLINE=1: each workgroup makes the plan itself at batches of at most 64 rows (no plan launch);
+- both of those: one launch a step, the finished-split counts tagged with the call's tag instead of cleared;
 - SILVANN_GFX950_DECODE_VTR=1: the V^T operand through the transposing LDS read at head_dim <= 256.
 
 A switch is read once a process, so the whole decode suite (tests/test_gpu_decode.py: the oracle, the torch fp32
@@ -20,20 +21,22 @@ pytestmark = pytest.mark.gpu
 HERE = Path(__file__).resolve().parent
 
 
-SUITES = {
-    "SILVANN_GFX950_DECODE_FUSED": ["test_gpu_decode.py"],
-    "SILVANN_GFX950_DECODE_INLINE": ["test_gpu_decode.py", "test_gpu_chains.py", "test_gpu_latent.py"],
-    "SILVANN_GFX950_DECODE_VTR": ["test_gpu_decode.py"],
+SUITES = {   # name: (switches, suites)
+    "fused": ({"SILVANN_GFX950_DECODE_FUSED": "1"}, ["test_gpu_decode.py"]),
+    "inline": ({"SILVANN_GFX950_DECODE_INLINE": "1"}, ["test_gpu_decode.py", "test_gpu_chains.py", "test_gpu_latent.py"]),
+    "one-launch": ({"SILVANN_GFX950_DECODE_FUSED": "1", "SILVANN_GFX950_DECODE_INLINE": "1"}, ["test_gpu_decode.py"]),
+    "vtr": ({"SILVANN_GFX950_DECODE_VTR": "1"}, ["test_gpu_decode.py"]),
 }
 
 
 @pytest.mark.timeout(400)
-@pytest.mark.parametrize("switch", list(SUITES))
-def test_decode_suite_with(dev, switch):
-    print(f"case: {' '.join(SUITES[switch])} with {switch}=1 (child process)", flush=True)
-    cmd = [sys.executable, "-u", "-m", "pytest", *[str(HERE / f) for f in SUITES[switch]], "-m", "gpu", "-x", "-q",
+@pytest.mark.parametrize("name", list(SUITES))
+def test_decode_suite_with(dev, name):
+    switches, files = SUITES[name]
+    print(f"case: {' '.join(files)} with {switches} (child process)", flush=True)
+    cmd = [sys.executable, "-u", "-m", "pytest", *[str(HERE / f) for f in files], "-m", "gpu", "-x", "-q",
            "-p", "no:cacheprovider", "--timeout", "120", "--timeout-method", "thread"]
-    r = subprocess.run(cmd, cwd=str(HERE.parent), env={**os.environ, switch: "1"},
+    r = subprocess.run(cmd, cwd=str(HERE.parent), env={**os.environ, **switches},
                        capture_output=True, text=True, timeout=360)
     print(r.stdout[-4000:], r.stderr[-2000:], flush=True)
     assert r.returncode == 0
