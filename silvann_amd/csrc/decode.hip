@@ -681,6 +681,15 @@ bool vtr() {
     return on;
 }
 
+// The fused finish (SILVANN_GFX950_DECODE_FUSED=1): checked in the CPU emulation, not yet measured on a GPU.
+bool fused_finish() {
+    static const bool on = [] {
+        const char* e = getenv("SILVANN_GFX950_DECODE_FUSED");
+        return e && strtol(e, nullptr, 10) > 0;
+    }();
+    return on;
+}
+
 // This call's tag for the fused finish's tagged counts: a process-wide serial from a random start, 40 bits, so a
 // count word left by another call (or any earlier contents of the scratch) shows another tag but by a 2^-40 chance.
 uint64_t next_tag() {
@@ -781,11 +790,7 @@ void decode_paged_launch(uint16_t* o, const uint16_t* q, const uint16_t* k, cons
     // measured: one workgroup an item beats the queue at both benchmark shapes (C2 5.17 vs 4.87 TB/s,
     // C5 6.2 vs 5.1), so the queue is opt-in
     const bool persistent = mode > 0;
-    // the fused finish (SILVANN_GFX950_DECODE_FUSED=1): checked in the CPU emulation, not yet measured on a GPU
-    static const bool fused = [] {
-        const char* e = getenv("SILVANN_GFX950_DECODE_FUSED");
-        return e && strtol(e, nullptr, 10) > 0;
-    }();
+    const bool fused = fused_finish();
     if (fused && head_dim <= 256 && !persistent && inline_plan() && rows <= 64) {
         // one launch: the plan made in the kernel, the counts tagged with this call's tag
         a.tag = next_tag();
@@ -935,6 +940,19 @@ bool decode_one(uint16_t* o, float* res, const uint16_t* q, const uint16_t* k, c
     a.tag = 0;
     hipStream_t st = stream();
     prof_begin(kProfDecodeSplit);
+    if (o && !sink && head_dim <= 256 && inline_plan() && fused_finish()) {
+        // one launch: the last split of each head block finishes the answers, its counts tagged
+        a.lens = nullptr;
+        a.len_first = (uint32_t)length;
+        a.lens_out = lens;
+        a.tag = next_tag();
+        const dim3 grid((uint32_t)(nsplit * kv_heads * hblocks));
+        if (head_dim == 256) decode_split<256, kDefaultVariant, false, false, false, true, false, true><<<grid, kThreads, 0, st>>>(a);
+        else if (head_dim == 128) decode_split<128, kDefaultVariant, false, false, false, true, false, true><<<grid, kThreads, 0, st>>>(a);
+        else decode_split<64, kDefaultVariant, false, false, false, true, false, true><<<grid, kThreads, 0, st>>>(a);
+        prof_end(kProfDecodeSplit);
+        return true;
+    }
     if (inline_plan()) {   // the length from the host, written out for the merge by the split kernel
         a.lens = nullptr;
         a.len_first = (uint32_t)length;

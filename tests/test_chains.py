@@ -244,3 +244,18 @@ def test_latent_chains_with_inline_plan(oracle):
     wp = oracle.softmax_lens(raw, p_row, lens, qh, rows)
     parity(o, oracle.mix_rows(qh * hd, wp, p_row, lat, most * hd, lens, qh, 1, hd, rows)[0])
     assert over == 0 and not [x for x in _launched(log) if x.startswith(PLANS)]
+
+
+@pytest.mark.parametrize("qh,kvh,hd,length", [(16, 2, 256, 2048), (8, 2, 128, 3000), (8, 8, 64, 700)])
+def test_decode_pair_in_one_launch(oracle, qh, kvh, hd, length):
+    """The decode verb's pair (attention_scores + attention_mix) with the fused finish and the inline plan on: one
+    decode_split launch, its finished-split counts tagged in the weights buffer (whatever it held), the answers the
+    oracle's."""
+    q, k, v = _inputs(qh + hd + length + 2, qh, kvh, hd, length)
+    env = {**INLINE, "SILVANN_GFX950_DECODE_FUSED": "1"}
+    o, p, _, over, log = emu.run_chain("decode", q, k, v, qh, kvh, hd, length, extra_env=env)
+    want_o, _ = oracle.mix(oracle.scores(q, k, qh, kvh, hd, length), v, qh, kvh, hd, length)
+    parity(o, want_o)
+    assert over == 0
+    launched = _launched(log)
+    assert len(launched) == 1 and "decode_split" in launched[0], launched

@@ -24,7 +24,8 @@ HERE = Path(__file__).resolve().parent
 SUITES = {   # name: (switches, suites)
     "fused": ({"SILVANN_GFX950_DECODE_FUSED": "1"}, ["test_gpu_decode.py"]),
     "inline": ({"SILVANN_GFX950_DECODE_INLINE": "1"}, ["test_gpu_decode.py", "test_gpu_chains.py", "test_gpu_latent.py"]),
-    "one-launch": ({"SILVANN_GFX950_DECODE_FUSED": "1", "SILVANN_GFX950_DECODE_INLINE": "1"}, ["test_gpu_decode.py"]),
+    "one-launch": ({"SILVANN_GFX950_DECODE_FUSED": "1", "SILVANN_GFX950_DECODE_INLINE": "1"},
+                   ["test_gpu_decode.py", "test_gpu_chains.py"]),
     "vtr": ({"SILVANN_GFX950_DECODE_VTR": "1"}, ["test_gpu_decode.py"]),
 }
 
