@@ -438,6 +438,10 @@ def main():
         secondary.append(isolated(2, a.steps, a.warmup,
                                   env={"SILVANN_GFX950_DECODE_INLINE": "1", "SILVANN_GFX950_DECODE_FUSED": "1"},
                                   variant="one launch a step (inline plan + fused finish)"))
+        for n in (1, 5):   # the launch-bound and the longest decode in one launch
+            secondary.append(isolated(n, max(5, a.steps // 2), a.warmup,
+                                      env={"SILVANN_GFX950_DECODE_INLINE": "1", "SILVANN_GFX950_DECODE_FUSED": "1"},
+                                      variant="one launch a step (inline plan + fused finish)"))
         for n in (10, 11):
             secondary.append(isolated(n, max(5, a.steps // 2), a.warmup))
     cpu = None if a.no_cpu else cpu_baseline(w2, a.cpu_threads)
