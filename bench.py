@@ -21,9 +21,9 @@ latent attention (64 heads over 131,072 512-wide latents, row 137 with k = v) in
 
 The TurboQuant, writer and latent lines run as child processes (`--only 6`..`9`), each under a time limit, so a
 failure there is recorded in its entry and cannot take the headline down; so does C2 once more with the split-K
-decode's opt-in candidates for its default (the fused finish, SILVANN_GFX950_DECODE_FUSED=1; the transposing V^T
-reads, SILVANN_GFX950_DECODE_VTR=1; the plan made inside decode_split, SILVANN_GFX950_DECODE_INLINE=1; the last two
-together, one launch a step), and C5 / C3 through the
+decode's opt-in candidates for its default with `--variants` (the fused finish, SILVANN_GFX950_DECODE_FUSED=1; the
+transposing V^T reads, SILVANN_GFX950_DECODE_VTR=1; the plan made inside decode_split, SILVANN_GFX950_DECODE_INLINE=1;
+the last two together, one launch a step, at C2, C1 and C5), and C5 / C3 through the
 reference's own decode and rows verbs, whose door chains this library defers and runs fused.
 
 `cpu_baseline` is the reference's own x86_avx2 silicon family (oracle/_ref, built from the reference's
@@ -59,6 +59,9 @@ def parse():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-secondary", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--variants", action="store_true",
+                    help="also the decode's opt-in candidates (fused finish, transposing reads, inline plan, one "
+                         "launch) as child-process lines")
     ap.add_argument("--cpu-threads", type=int, default=int(os.environ.get("BENCH_CPU_THREADS", "16")))
     ap.add_argument("--only", type=int, default=0,
                     help="time only this config (1-5: BASELINE.json's; 6, 7: a 4-bit / 8-bit TurboQuant tier; 8: the "
@@ -429,19 +432,20 @@ def main():
         torch.cuda.empty_cache()
         for n in sorted([*W.TIERS, *W.WRITES, *W.LATENTS]):
             secondary.append(isolated(n, max(5, a.steps // 2), a.warmup))
-        secondary.append(isolated(2, a.steps, a.warmup, env={"SILVANN_GFX950_DECODE_FUSED": "1"},
-                                  variant="fused finish (no merge launch)"))
-        secondary.append(isolated(2, a.steps, a.warmup, env={"SILVANN_GFX950_DECODE_VTR": "1"},
-                                  variant="transposing V^T reads"))
-        secondary.append(isolated(2, a.steps, a.warmup, env={"SILVANN_GFX950_DECODE_INLINE": "1"},
-                                  variant="plan inside decode_split (no plan launch)"))
-        secondary.append(isolated(2, a.steps, a.warmup,
-                                  env={"SILVANN_GFX950_DECODE_INLINE": "1", "SILVANN_GFX950_DECODE_FUSED": "1"},
-                                  variant="one launch a step (inline plan + fused finish)"))
-        for n in (1, 5):   # the launch-bound and the longest decode in one launch
-            secondary.append(isolated(n, max(5, a.steps // 2), a.warmup,
+        if a.variants:
+            secondary.append(isolated(2, a.steps, a.warmup, env={"SILVANN_GFX950_DECODE_FUSED": "1"},
+                                      variant="fused finish (no merge launch)"))
+            secondary.append(isolated(2, a.steps, a.warmup, env={"SILVANN_GFX950_DECODE_VTR": "1"},
+                                      variant="transposing V^T reads"))
+            secondary.append(isolated(2, a.steps, a.warmup, env={"SILVANN_GFX950_DECODE_INLINE": "1"},
+                                      variant="plan inside decode_split (no plan launch)"))
+            secondary.append(isolated(2, a.steps, a.warmup,
                                       env={"SILVANN_GFX950_DECODE_INLINE": "1", "SILVANN_GFX950_DECODE_FUSED": "1"},
                                       variant="one launch a step (inline plan + fused finish)"))
+            for n in (1, 5):   # the launch-bound and the longest decode in one launch
+                secondary.append(isolated(n, max(5, a.steps // 2), a.warmup,
+                                          env={"SILVANN_GFX950_DECODE_INLINE": "1", "SILVANN_GFX950_DECODE_FUSED": "1"},
+                                          variant="one launch a step (inline plan + fused finish)"))
         for n in (10, 11):
             secondary.append(isolated(n, max(5, a.steps // 2), a.warmup))
     cpu = None if a.no_cpu else cpu_baseline(w2, a.cpu_threads)
