@@ -255,8 +255,9 @@ void* silvann_gfx950_get_stream(void);
  * scratch). Any other door of this library — and set_stream, launch_failed, flush — first runs what is recorded
  * exactly as the door would have run, so any other order of calls keeps the reference's semantics. A caller that
  * reads `p` itself after a chain's first door, or that calls a door of another library in between, calls
- * silvann_gfx950_flush() first, or switches deferral off for its thread. SILVANN_GFX950_DEFER=0 makes off the
- * process default. (No counterpart in the reference: the fusion its door ABI leaves no single door for.) */
+ * silvann_gfx950_flush() first, or switches deferral off for its thread; so does a family's wait (compute_completed)
+ * before it synchronises, and a thread before it ends. SILVANN_GFX950_DEFER=0 makes off the process default. (No
+ * counterpart in the reference: the fusion its door ABI leaves no single door for.) */
 void silvann_gfx950_flush(void);
 void silvann_gfx950_set_defer(int on);
 /* Nonzero if a door on the current device refused its operands or failed to launch since the last call; clears
