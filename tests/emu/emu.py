@@ -8,6 +8,7 @@ C entry point in the emulation and return the fp16 answer and the fault word.
 from __future__ import annotations
 
 import concurrent.futures as cf
+import fcntl
 import hashlib
 import os
 import shutil
@@ -42,6 +43,18 @@ def _digest() -> str:
 
 
 def build() -> Path:
+    """Build under an exclusive lock: pytest-xdist workers would otherwise regenerate and compile the same files
+    at once (a source rewritten while clang reads it)."""
+    BUILD.mkdir(parents=True, exist_ok=True)
+    with open(BUILD / ".lock", "w") as lk:
+        fcntl.flock(lk, fcntl.LOCK_EX)
+        try:
+            return _build_locked()
+        finally:
+            fcntl.flock(lk, fcntl.LOCK_UN)
+
+
+def _build_locked() -> Path:
     from . import gen
     cxx = compiler()
     if cxx is None:
