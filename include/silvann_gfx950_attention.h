@@ -160,6 +160,8 @@ void silvann_gfx950_rope_rows(uint16_t* o, const uint16_t* x, const float* cs, u
  * `silvann_gfx950_attention_decode_paged_scratch` bytes (0 if it needs none). `page_size` a multiple of 16
  * positions (of 32 for the causal row). `most` is the largest lens[u]
  * (a bound the grid is sized by; lens[u] <= most is the caller's promise). A row with lens[u] == 0 answers 0.
+ * q, k and v 16-byte aligned, k_row a multiple of 8 halves and scratch 8-byte aligned; other operands are
+ * refused (nothing launched, the refusal remembered for silvann_gfx950_launch_failed).
  * Split-K form of the reference's decode verb (engine/src/packages/nn/cpu/opcodes/attention__abi.cuh:129-160),
  * many rows as `attention_scores_grouped_rows` (gpu.cuh:222) takes them. */
 #define SILVANN_GFX950_ROW_ATTENTION_DECODE_PAGED 137u
@@ -177,7 +179,8 @@ uint64_t silvann_gfx950_attention_decode_paged_scratch(uint64_t q_heads, uint64_
  * cache). The fused form of `attention_causal_scores_grouped` + `attention_causal_softmax` +
  * `attention_causal_mix` (gpu.cuh:191,192,156) as the reference's `nn__attention__rows` runs them
  * (attention__abi.cuh:407-414), on fp16 MFMA with fp32 accumulation; no weights are materialised.
- * first + rows < 2^31 and page_size a multiple of 32 below 2^31; other shapes are refused (nothing launched,
+ * first + rows < 2^31, page_size a multiple of 32 below 2^31, q, k and v 16-byte aligned; other shapes are
+ * refused (nothing launched,
  * the refusal remembered for silvann_gfx950_launch_failed). */
 #define SILVANN_GFX950_ROW_ATTENTION_CAUSAL_PAGED 138u
 void silvann_gfx950_attention_causal_paged(uint16_t* o, const uint16_t* q, const uint16_t* k, const uint16_t* v,
@@ -220,7 +223,8 @@ void silvann_gfx950_attention_cache_write_paged(uint16_t* k_cache, uint16_t* v_c
  * leave in `res`, for `rows` query rows over the same `length` TurboQuant key and value rows — row u's q_heads at
  * q + u·q_heads·head_dim, its residuals at res + u·q_heads·(head_dim + 2) — as `attention_weights_tq_rows` +
  * `attention_residual_mix_tq_rows` (gpu.cuh:197-198) give them. Codes as in row 69; d is 4 or 8 (the tiers' widths,
- * attention__abi.cuh:258); head_dim 64, 128 or 256; the code planes 8-byte aligned; other operands are refused.
+ * attention__abi.cuh:258); head_dim 64, 128 or 256; the code planes 8-byte and q 16-byte aligned; other operands
+ * are refused.
  * Split-K on MFMA: no weights are materialised and every code is read once. `scratch` holds the splits' residuals,
  * `silvann_gfx950_attention_residual_tq_scratch` bytes. The tiers' verbs call weights_tq then residual_mix_tq then
  * merge (mixer__abi.cuh:395-410); this row replaces the first two. */
@@ -252,7 +256,8 @@ void* silvann_gfx950_get_stream(void);
  * library records such a chain's first doors instead of launching them; when the continuation arrives on the same
  * thread and stream with the same operands, the chain runs as one fused kernel (the split-K decode of row 137, the
  * causal prefill of row 138) and the weights buffer `p` never holds weights (the decode pairs use it as their
- * scratch). Any other door of this library — and set_stream, launch_failed, flush — first runs what is recorded
+ * scratch; the fused forms run only when q, k and v are 16-byte aligned and `p` 8-byte aligned, else the doors run
+ * one by one). Any other door of this library — and set_stream, launch_failed, flush — first runs what is recorded
  * exactly as the door would have run, so any other order of calls keeps the reference's semantics. A caller that
  * reads `p` itself after a chain's first door, or that calls a door of another library in between, calls
  * silvann_gfx950_flush() first, or switches deferral off for its thread; so does a family's wait (compute_completed)

@@ -144,6 +144,12 @@ bool decode_causal(uint16_t* o, const uint16_t* q, const uint16_t* k, const uint
 bool residual_tq_fit(float* res, const uint16_t* q, const uint8_t* kc, const uint16_t* ks, const uint8_t* vc,
                      const uint16_t* vs, uint64_t q_heads, uint64_t kv_heads, uint64_t head_dim, uint64_t length,
                      uint64_t d, uint64_t rows, void* scratch, uint64_t cap);
+// The fused kernels read q and the K and V rows in 16-byte vectors (and V through 16-byte LDS-DMA), and keep 64-bit
+// counters in their scratch: a fused form runs only on operands aligned for that, else the doors run one by one.
+inline bool vec_aligned(const void* q, const void* k, const void* v) {
+    return (((uintptr_t)q | (uintptr_t)k | (uintptr_t)v) & 15u) == 0;
+}
+inline bool scratch_aligned(const void* s) { return (((uintptr_t)s) & 7u) == 0; }
 bool causal_shape_ok(uint64_t q_heads, uint64_t kv_heads, uint64_t head_dim, uint64_t first, uint64_t rows,
                      bool paged, uint64_t page_size);
 void causal_paged_launch(uint16_t* o, float* res, const uint16_t* q, const uint16_t* k, const uint16_t* v,

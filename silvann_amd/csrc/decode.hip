@@ -731,7 +731,7 @@ void split_contiguous(const DecodeArgs& a, uint64_t head_dim, bool shared, uint6
 uint32_t head_blocks(uint64_t q_heads, uint64_t kv_heads) { return (uint32_t)((q_heads / kv_heads + 15) / 16); }
 
 bool decode_shape_ok(uint64_t q_heads, uint64_t kv_heads, uint64_t head_dim, uint64_t most, uint64_t rows) {
-    return (head_dim == 64 || head_dim == 128 || head_dim == 256 || head_dim == 512) && kv_heads > 0 && q_heads % kv_heads == 0 &&
+    return (head_dim == 64 || head_dim == 128 || head_dim == 256 || head_dim == 512) && kv_heads > 0 && q_heads > 0 && q_heads % kv_heads == 0 &&
            rows > 0 && rows <= 65535 && most > 0 && most < (1ull << 31) && kv_heads * head_blocks(q_heads, kv_heads) <= 65535;
 }
 
@@ -746,6 +746,12 @@ void decode_paged_launch(uint16_t* o, const uint16_t* q, const uint16_t* k, cons
                         "head_dim %llu most %llu rows %llu page_size %llu)\n",
                 (unsigned long long)q_heads, (unsigned long long)kv_heads, (unsigned long long)head_dim,
                 (unsigned long long)most, (unsigned long long)rows, (unsigned long long)page_size);
+        refuse("attention_decode_paged");
+        return;
+    }
+    if (!vec_aligned(q, k, v) || !scratch_aligned(scratch) || k_row % 8 != 0) {
+        fprintf(stderr, "silvann_gfx950: attention_decode_paged: q, k and v must be 16-byte aligned, k_row a multiple "
+                        "of 8 elements and scratch 8-byte aligned\n");
         refuse("attention_decode_paged");
         return;
     }
@@ -909,7 +915,8 @@ bool decode_one(uint16_t* o, float* res, const uint16_t* q, const uint16_t* k, c
                 uint64_t kv_heads, uint64_t head_dim, uint64_t length, void* scratch, uint64_t cap, unsigned int* over,
                 const uint16_t* sink) {
     if (sink && !o) return false;   // a sink weighs the answer's sum; the residual form has none
-    if (!decode_shape_ok(q_heads, kv_heads, head_dim, length, 1) || (((uintptr_t)scratch) & 3u) != 0) return false;
+    if (!decode_shape_ok(q_heads, kv_heads, head_dim, length, 1) || !vec_aligned(q, k, v) || !scratch_aligned(scratch))
+        return false;
     const uint32_t hblocks = head_blocks(q_heads, kv_heads);
     const uint64_t head = part_at(1, kv_heads * hblocks), per_split = q_heads * (head_dim + 2) * sizeof(float);
     if (cap <= head || (cap - head) / per_split == 0) return false;
@@ -999,7 +1006,8 @@ bool decode_causal(uint16_t* o, const uint16_t* q, const uint16_t* k, const uint
                    uint64_t kv_heads, uint64_t head_dim, uint64_t first, uint64_t rows, void* scratch, uint64_t cap,
                    unsigned int* over) {
     const uint64_t most = first + rows;
-    if (!decode_shape_ok(q_heads, kv_heads, head_dim, most, rows) || (((uintptr_t)scratch) & 3u) != 0) return false;
+    if (!decode_shape_ok(q_heads, kv_heads, head_dim, most, rows) || !vec_aligned(q, k, v) || !scratch_aligned(scratch))
+        return false;
     const uint32_t hblocks = head_blocks(q_heads, kv_heads);
     const uint64_t lens_at = part_at(rows, kv_heads * hblocks);
     const uint64_t head = lens_at + (4 * rows + 255) / 256 * 256;
@@ -1066,7 +1074,9 @@ bool decode_causal(uint16_t* o, const uint16_t* q, const uint16_t* k, const uint
 bool decode_rows_fit(uint16_t* o, const uint16_t* q, const uint16_t* k, const uint16_t* v, const uint32_t* lens,
                      uint64_t k_row, uint64_t q_heads, uint64_t kv_heads, uint64_t head_dim, uint64_t most,
                      uint64_t rows, void* scratch, uint64_t cap, unsigned int* over) {
-    if (!decode_shape_ok(q_heads, kv_heads, head_dim, most, rows) || (((uintptr_t)scratch) & 3u) != 0) return false;
+    if (!decode_shape_ok(q_heads, kv_heads, head_dim, most, rows) || !vec_aligned(q, k, v) || !scratch_aligned(scratch) ||
+        k_row % 8 != 0)
+        return false;
     const uint32_t hblocks = head_blocks(q_heads, kv_heads);
     const uint64_t head = part_at(rows, kv_heads * hblocks);
     const uint64_t per_split = rows * q_heads * (head_dim + 2) * sizeof(float);

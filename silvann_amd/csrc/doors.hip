@@ -832,7 +832,7 @@ SILVANN_EXPORT void silvann_gfx950_attention_causal_mix(uint16_t* o, const float
     if (d.kind == kDeferCausalSoftmax && d.p == p && d.q_heads == q_heads && d.kv_heads == kv_heads &&
         d.head_dim == head_dim && d.first == first && d.rows == rows && d.st == stream()) {
         const Deferred r = d;
-        if (causal_shape_ok(q_heads, kv_heads, head_dim, first, rows, false, 0)) {
+        if (causal_shape_ok(q_heads, kv_heads, head_dim, first, rows, false, 0) && vec_aligned(r.q, r.k, v)) {
             d = Deferred();   // the chain runs fused on the matrix cores: p is never written
             causal_paged_launch(o, nullptr, r.q, r.k, v, nullptr, 0, q_heads, kv_heads, head_dim, first, rows, over,
                                 "attention_causal_mix");
@@ -943,7 +943,7 @@ SILVANN_EXPORT void silvann_gfx950_attention_residual_mix_rows(float* res, const
                                                                uint64_t first, uint64_t rows) {
     Deferred& d = deferred();
     if (d.kind == kDeferWeightsRows && d.p == p && d.res == res && d.q_heads == q_heads && d.kv_heads == kv_heads &&
-        d.head_dim == head_dim && d.first == first && d.rows == rows && d.st == stream()) {
+        d.head_dim == head_dim && d.first == first && d.rows == rows && d.st == stream() && vec_aligned(d.q, d.k, v)) {
         const Deferred r = d;
         d = Deferred();   // the pair runs fused: p is never written
         causal_paged_launch(nullptr, res, r.q, r.k, v, nullptr, 0, q_heads, kv_heads, head_dim, first, rows, nullptr,

@@ -821,7 +821,8 @@ static bool prefill_pipe() {
 // The shapes causal_mfma takes (pages NULL or `page_size` positions a page).
 bool causal_shape_ok(uint64_t q_heads, uint64_t kv_heads, uint64_t head_dim, uint64_t first, uint64_t rows,
                      bool paged, uint64_t page_size) {
-    return (head_dim == 64 || head_dim == 128 || head_dim == 256) && kv_heads > 0 && q_heads % kv_heads == 0 &&
+    return (head_dim == 64 || head_dim == 128 || head_dim == 256) && kv_heads > 0 && q_heads > 0 &&
+           q_heads % kv_heads == 0 &&
            rows > 0 && first + rows < (1ull << 31) &&
            (!paged || (page_size > 0 && page_size < (1ull << 31) && page_size % kKT == 0));
 }
@@ -831,6 +832,11 @@ void causal_paged_launch(uint16_t* o, float* res, const uint16_t* q, const uint1
                          const uint32_t* pages, uint64_t page_size, uint64_t q_heads, uint64_t kv_heads,
                          uint64_t head_dim, uint64_t first, uint64_t rows, unsigned int* over, const char* what) {
     if (!causal_shape_ok(q_heads, kv_heads, head_dim, first, rows, pages != nullptr, page_size)) {
+        refuse(what);
+        return;
+    }
+    if (!vec_aligned(q, k, v)) {
+        fprintf(stderr, "silvann_gfx950: %s: q, k and v must be 16-byte aligned\n", what);
         refuse(what);
         return;
     }

@@ -335,7 +335,8 @@ void residual_tq_run(float* res, const uint16_t* q, const uint8_t* kc, const uin
 void residual_tq_launch(float* res, const uint16_t* q, const uint8_t* kc, const uint16_t* ks, const uint8_t* vc,
                         const uint16_t* vs, uint64_t q_heads, uint64_t kv_heads, uint64_t head_dim, uint64_t length,
                         uint64_t d, uint64_t rows, float* scratch) {
-    if (!tq_shape_ok(q_heads, kv_heads, head_dim, length, d, rows) || (((uintptr_t)kc | (uintptr_t)vc) & 7u) != 0) {
+    if (!tq_shape_ok(q_heads, kv_heads, head_dim, length, d, rows) || (((uintptr_t)kc | (uintptr_t)vc) & 7u) != 0 ||
+        (((uintptr_t)q) & 15u) != 0) {
         refuse("attention_residual_tq");
         return;
     }
@@ -354,7 +355,8 @@ bool residual_tq_fit(float* res, const uint16_t* q, const uint8_t* kc, const uin
                      const uint16_t* vs, uint64_t q_heads, uint64_t kv_heads, uint64_t head_dim, uint64_t length,
                      uint64_t d, uint64_t rows, void* scratch, uint64_t cap) {
     if (!tq_shape_ok(q_heads, kv_heads, head_dim, length, d, rows) || length == 0 ||
-        (((uintptr_t)kc | (uintptr_t)vc) & 7u) != 0 || (((uintptr_t)scratch) & 3u) != 0)
+        (((uintptr_t)kc | (uintptr_t)vc) & 7u) != 0 || (((uintptr_t)q) & 15u) != 0 ||
+        !scratch_aligned(scratch))
         return false;
     const uint64_t per_split = rows * q_heads * (head_dim + 2) * sizeof(float);
     const uint64_t fit = cap / per_split;

@@ -97,7 +97,16 @@ int main(int argc, char** argv) {
         return 2;
     fclose(fp);
     alarm((unsigned)timeout);
-    char* q = load(d + "/q.bin", "q");
+    size_t qn = 0;
+    char* q = load(d + "/q.bin", "q", &qn);
+    // EMU_MISALIGN=q: q moved to an address 2 mod 16; =p: the chains' weights buffer at 4 mod 8
+    const char* mis = getenv("EMU_MISALIGN");
+    const bool mis_q = mis && std::string(mis) == "q", mis_p = mis && std::string(mis) == "p";
+    if (mis_q && q) {
+        char* m = guarded(qn + 2, "q");   // ends 2 bytes short of the page: starts at 2 mod 16 for qn a multiple of 16
+        memcpy(m, q, qn);
+        q = m;
+    }
     char* k = load(d + "/k.bin", "k");
     char* v = load(d + "/v.bin", "v");
     if (!v) v = k;   // no values of their own: the keys are the values (latent attention)
@@ -176,7 +185,7 @@ int main(int argc, char** argv) {
         // SILVANN_GFX950_DEFER=0): scores then mix into o, or weights then residual_mix into res. a1 = 1 puts a
         // merge of an unrelated pair of residuals between the two doors (which must run the first door as it was).
         const unsigned long length = a0, rf = hd + 2;
-        float* p = (float*)guarded(qh * length * 4, "p");
+        float* p = (float*)guarded(qh * length * 4 + (mis_p ? 4 : 0), "p");
         memset(p, 0xFF, qh * length * 4);
         float* res = (float*)guarded(qh * rf * 4, "res");
         memset(res, 0xFF, qh * rf * 4);

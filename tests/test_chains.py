@@ -259,3 +259,29 @@ def test_decode_pair_in_one_launch(oracle, qh, kvh, hd, length):
     assert over == 0
     launched = _launched(log)
     assert len(launched) == 1 and "decode_split" in launched[0], launched
+
+
+@pytest.mark.parametrize("kind,misalign", [("decode", "q"), ("decode", "p"), ("causal", "q")])
+def test_unaligned_operands_run_door_by_door(oracle, kind, misalign):
+    """The fused forms read q, K and V in 16-byte vectors and keep 64-bit counters in the weights buffer: a q at
+    2 mod 16, or a weights buffer at 4 mod 8, makes the chain run door by door (the buffer then holds the oracle's
+    weights) with the same answers."""
+    env = {"EMU_MISALIGN": misalign}
+    if kind == "decode":
+        qh, kvh, hd, length = 16, 2, 256, 2048
+        q, k, v = _inputs(91, qh, kvh, hd, length)
+        o, p, _, over, _ = emu.run_chain("decode", q, k, v, qh, kvh, hd, length, extra_env=env)
+        want_p = oracle.scores(q, k, qh, kvh, hd, length)
+        want_o, _ = oracle.mix(want_p, v, qh, kvh, hd, length)
+    else:
+        qh, kvh, hd, first, rows = 16, 2, 256, 77, 95
+        q, k, v = _inputs(92, qh, kvh, hd, first + rows, rows)
+        o, p, over, _ = emu.run_chain("causal", q, k, v, qh, kvh, hd, first, rows, extra_env=env)
+        want_o, _ = oracle.causal_rows(q, k, v, None, 0, qh, kvh, hd, first, list(range(rows)))
+        want_p = oracle.causal_softmax(oracle.causal_scores_grouped(q, k, qh, kvh, hd, first, rows), qh, first, rows)
+        # row r's weights are its first + r + 1 positions; past them the buffer keeps what it held
+        valid = (np.arange(first + rows)[None, :] <= first + np.repeat(np.arange(rows), qh)[:, None]).ravel()
+        p, want_p = p[valid], want_p[valid]
+    parity(o, want_o)
+    assert over == 0
+    np.testing.assert_allclose(p, want_p, rtol=1e-4, atol=1e-6)

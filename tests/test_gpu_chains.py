@@ -190,3 +190,29 @@ def test_latent_decode_chain_runs_fused(dev, oracle, heads, length, sink):
     assert int(over.item()) == 0
     assert not np.allclose(p.cpu().numpy(), wp, rtol=1e-4, atol=1e-6)   # fused: no weights were written
     assert not doors.launch_failed()
+
+
+@pytest.mark.parametrize("misalign", ["q", "p"])
+def test_unaligned_decode_chain_runs_door_by_door(dev, oracle, misalign):
+    """With deferral on, a q at 2 mod 16 (a view one half into its buffer) or a weights buffer at 4 mod 8 keeps the
+    decode verb's pair off the fused kernel, whose 16-byte loads and 64-bit counters need alignment: each door runs
+    on its own, the weights buffer holds the oracle's weights and the answers meet it."""
+    qh, kvh, hd, L = 16, 2, 256, 2048
+    print(f"case: decode chain, {misalign} misaligned", flush=True)
+    q, k, v = _decode_case(43, qh, kvh, hd, L)
+    qd = t(q, dev)
+    if misalign == "q":
+        qbuf = _z(dev, qh * hd + 8, torch.float16)
+        qbuf[1:1 + qh * hd] = qd
+        qd = qbuf[1:1 + qh * hd]
+    sbuf = _z(dev, qh * L + 2)
+    scores = sbuf[1:1 + qh * L] if misalign == "p" else sbuf[:qh * L]
+    out, over = _z(dev, qh * hd, torch.float16), _z(dev, 1, torch.int32)
+    assert (qd.data_ptr() % 16 != 0) == (misalign == "q") and (scores.data_ptr() % 8 != 0) == (misalign == "p")
+    verbs.decode(qd, t(k, dev), t(v, dev), scores, out, qh, kvh, hd, 0, L, over)
+    want_p = oracle.scores(q, k, qh, kvh, hd, L)
+    want_o, _ = oracle.mix(want_p, v, qh, kvh, hd, L)
+    parity(out.cpu().numpy(), want_o)
+    assert int(over.item()) == 0
+    np.testing.assert_allclose(scores.cpu().numpy(), want_p, rtol=1e-5, atol=1e-7)
+    assert not doors.launch_failed()

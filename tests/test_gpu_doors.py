@@ -168,6 +168,36 @@ def test_refused_shape_launches_nothing(dev):
     assert torch.all(o == 7.0) and int(over.item()) == 0
 
 
+def test_refused_operands_of_the_appended_rows(dev):
+    """Rows 137 and 138 refuse, launching nothing, q_heads 0 (0 % kv_heads is 0, which a divisibility check alone lets
+    through to a zero-size grid), an unaligned q or k (their kernels load 16 bytes at a time) and, for 137, a scratch
+    at 4 mod 8 (its counters are 64-bit)."""
+    doors.launch_failed()
+    o = torch.full((16 * 128,), 7.0, dtype=torch.float16, device=dev)
+    q = torch.zeros(16 * 128 + 8, dtype=torch.float16, device=dev)
+    kv = torch.zeros(64 * 2 * 128 + 8, dtype=torch.float16, device=dev)
+    lens = torch.tensor([64], dtype=torch.int32, device=dev)
+    scratch = torch.zeros(1 << 20, dtype=torch.uint8, device=dev)
+    over = dev_zeros(1, torch.int32, dev)
+    cases = [
+        ("decode q_heads 0", lambda: doors.attention_decode_paged(o, q, kv, kv, None, 0, 0, 0, lens, 0, 2, 128, 64, 1,
+                                                                  scratch, over)),
+        ("decode q at 2 mod 16", lambda: doors.attention_decode_paged(o, q.data_ptr() + 2, kv, kv, None, 0, 0, 0, lens,
+                                                                      16, 2, 128, 64, 1, scratch, over)),
+        ("decode scratch at 4 mod 8", lambda: doors.attention_decode_paged(o, q, kv, kv, None, 0, 0, 0, lens, 16, 2,
+                                                                           128, 64, 1, scratch.data_ptr() + 4, over)),
+        ("causal q_heads 0", lambda: doors.attention_causal_paged(o, q, kv, kv, None, 0, 0, 2, 128, 0, 8, over)),
+        ("causal k at 2 mod 16", lambda: doors.attention_causal_paged(o, q, kv.data_ptr() + 2, kv, None, 0, 16, 2, 128,
+                                                                      0, 8, over)),
+    ]
+    for name, call in cases:
+        print(f"case: refusal, {name}", flush=True)
+        call()
+        torch.cuda.synchronize()
+        assert doors.launch_failed() == 1, name
+        assert torch.all(o == 7.0) and int(over.item()) == 0, name
+
+
 def test_lens_rows(dev, oracle):
     qh, kvh, hd, rows = 16, 4, 128, 5
     lens = np.array([7, 100, 1, 64, 250], np.uint32)
