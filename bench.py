@@ -6,25 +6,27 @@ Headline (`value`): config 2 of BASELINE.json — batched decode, 32 sequences w
 from the seed, 32 q / 4 kv heads, head_dim 128, fp16 K/V in 256-position pages under seeded permuted page
 tables — through the split-K decode door (silvann_gfx950_attention_decode_paged). A step is one decode of
 the whole batch; `value` is its algorithmic bytes (each cached K and V row once, plus q, o and the page
-table entries) × K over the wall time of the K steps, inputs resident in HBM.
+table entries) × K over the K steps' own durations, inputs resident in HBM. Before each timed step a 1 GiB
+buffer is written, so no step finds its inputs in the 256 MB Infinity Cache or the L2s; each step is bracketed
+by hipEvents on the null stream, the one the library launches on, and the flushes fall outside them
+(`wall_ms_per_step` in the lines is the wall clock of the whole timed region, flushes included).
 
 `roofline` is the dominant kernel's (decode_split): algorithmic bytes ÷ its average launch duration, timed
-live with hipEvents on the stream the library launches on, against 8 TB/s. `traffic` is the HBM bytes a
-launch moves per rocprofv3 FETCH_SIZE + WRITE_SIZE, read from profiles/traffic.json when it holds a
-measurement of this kernel and workload (else null).
+live with hipEvents on the stream the library launches on, against 8 TB/s; `step_frac` is the same bytes over
+the whole step (plan, split and merge launches and the gaps between them). `traffic` is the HBM bytes a launch
+moves per rocprofv3 FETCH_SIZE + WRITE_SIZE, read from profiles/traffic.json when it holds a measurement of
+this kernel and workload (else null).
 
 `secondary` holds the other configurations' lines (decode GB/s for C1 and C5; prefill TFLOP/s for C3 and
-C4 against 2.5 PFLOP/s dense fp16), each timed the same way, then the fused TurboQuant residual
-(attention_residual_tq) over a 4-bit and an 8-bit tier of C5's shape, in GB/s of codes, scales, q and residuals,
-the cache writer (attention_cache_write_paged) placing C4's 2,048-row chunk, keys turned, in GB/s, and GLM 5.3's
-latent attention (64 heads over 131,072 512-wide latents, row 137 with k = v) in GB/s with its TFLOP/s beside.
+C4 against 2.5 PFLOP/s dense fp16), each timed the same way.
 
-The TurboQuant, writer and latent lines run as child processes (`--only 6`..`9`), each under a time limit, so a
-failure there is recorded in its entry and cannot take the headline down; so does C2 once more with the split-K
-decode's opt-in candidates for its default with `--variants` (the fused finish, SILVANN_GFX950_DECODE_FUSED=1; the
-transposing V^T reads, SILVANN_GFX950_DECODE_VTR=1; the plan made inside decode_split, SILVANN_GFX950_DECODE_INLINE=1;
-the last two together, one launch a step, at C2, C1 and C5), and C5 / C3 through the
-reference's own decode and rows verbs, whose door chains this library defers and runs fused.
+With `--extra`, child processes (`--only 6`..`11`, each under a time limit, so a failure is recorded in its
+entry and cannot take the headline down) add the fused TurboQuant residual (attention_residual_tq) over a 4-bit
+and an 8-bit tier of C5's shape, in GB/s of codes, scales, q and residuals; the cache writer
+(attention_cache_write_paged) placing C4's 2,048-row chunk, keys turned, in GB/s; GLM 5.3's latent attention
+(64 heads over 131,072 512-wide latents, row 137 with k = v) in GB/s with its TFLOP/s beside; and C5 / C3
+through the reference's own decode and rows verbs, whose door chains this library defers and runs fused. With
+`--variants`, C2 once more with each of the split-K decode's opt-in forms.
 
 `cpu_baseline` is the reference's own x86_avx2 silicon family (oracle/_ref, built from the reference's
 sources) over the same batch, its doors called through its nn table on the host cores — both of the
@@ -62,6 +64,8 @@ def parse():
     ap.add_argument("--variants", action="store_true",
                     help="also the decode's opt-in candidates (fused finish, transposing reads, inline plan, one "
                          "launch) as child-process lines")
+    ap.add_argument("--extra", action="store_true",
+                    help="also the lines of the section-f rows and the reference verbs (--only 6..11) as child processes")
     ap.add_argument("--cpu-threads", type=int, default=int(os.environ.get("BENCH_CPU_THREADS", "16")))
     ap.add_argument("--only", type=int, default=0,
                     help="time only this config (1-5: BASELINE.json's; 6, 7: a 4-bit / 8-bit TurboQuant tier; 8: the "
@@ -82,9 +86,25 @@ def prof_read(name):
     return ms.value, n.value
 
 
+_FLUSH = {}
+
+
+def _flush_l2():
+    """Evict the caches between timed steps: write a 1 GiB buffer, four times the MI355X's 256 MB Infinity Cache
+    (MALL) and far beyond its L2s, so every step reads its inputs from HBM."""
+    import torch
+    buf = _FLUSH.get("buf")
+    if buf is None:
+        buf = _FLUSH["buf"] = torch.empty(1 << 28, dtype=torch.int32, device="cuda:0")
+    _FLUSH["n"] = _FLUSH.get("n", 0) + 1
+    buf.fill_(_FLUSH["n"])
+
+
 def time_steps(step, steps, warmup, kernel):
-    """Warm up, then time exactly `steps` steps: wall clock between device synchronisations, and the named
-    kernel's hipEvent durations on the library's stream."""
+    """Warm up, then time exactly `steps` steps, each after a cache flush: the steps' own durations (hipEvents on
+    the stream the library launches on, around each step, the flush outside them), the wall clock of the whole
+    timed region between device synchronisations (flushes included), and the named kernel's average launch
+    duration (the library's hipEvents around that kernel)."""
     import torch
     import silvann_amd
     L = silvann_amd.lib()
@@ -94,18 +114,25 @@ def time_steps(step, steps, warmup, kernel):
     L.silvann_gfx950_profile_enable(1)
     for k in KERNELS:
         prof_read(k)
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
+    stream = torch.cuda.current_stream()
+    assert stream.cuda_stream == 0, "the library launches on the null stream; time it there"
     torch.cuda.synchronize()
     t0 = time.perf_counter()
-    for _ in range(steps):
+    for a, b in evs:
+        _flush_l2()
+        a.record(stream)
         step()
+        b.record(stream)
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
     L.silvann_gfx950_profile_enable(0)
+    step_s = sum(a.elapsed_time(b) for a, b in evs) * 1e-3
     kms, n = prof_read(kernel)
     others = {k: prof_read(k) for k in KERNELS if k != kernel}
     if silvann_amd.doors.launch_failed():
         raise RuntimeError("a launch failed during the timed steps")
-    return wall, kms / max(n, 1), others
+    return {"step_s": step_s, "wall_s": wall}, kms / max(n, 1), others
 
 
 def traffic_for(kernel, workload):
@@ -152,24 +179,28 @@ def causal_setup(w, dev):
 
 def bench_decode(w, dev, steps, warmup):
     step, out, over = decode_setup(w, dev)
-    wall, split_ms, others = time_steps(step, steps, warmup, "decode_split")
+    tm, split_ms, others = time_steps(step, steps, warmup, "decode_split")
     b = w.io_bytes()
     merge_ms = others["decode_merge"][0] / max(others["decode_merge"][1], 1)
     return {
-        "config": w.name, "unit": "GB/s", "value": b * steps / wall / 1e9, "ms_per_step": wall / steps * 1e3,
+        "config": w.name, "unit": "GB/s", "value": b * steps / tm["step_s"] / 1e9,
+        "ms_per_step": tm["step_s"] / steps * 1e3, "wall_ms_per_step": tm["wall_s"] / steps * 1e3,
         "bytes_per_step": b, "split_ms": split_ms, "merge_ms": merge_ms,
         "kernel_gbs": b / (split_ms * 1e-3) / 1e9, "frac": b / (split_ms * 1e-3) / 1e9 / HBM_PEAK_GBS,
+        "step_frac": b * steps / tm["step_s"] / 1e9 / HBM_PEAK_GBS,
     }, out
 
 
 def bench_causal(w, dev, steps, warmup):
     step, out, over = causal_setup(w, dev)
-    wall, kms, _ = time_steps(step, steps, warmup, "causal_mfma")
+    tm, kms, _ = time_steps(step, steps, warmup, "causal_mfma")
     f = w.flops()
     return {
-        "config": w.name, "unit": "TFLOP/s", "value": f * steps / wall / 1e12, "ms_per_step": wall / steps * 1e3,
+        "config": w.name, "unit": "TFLOP/s", "value": f * steps / tm["step_s"] / 1e12,
+        "ms_per_step": tm["step_s"] / steps * 1e3, "wall_ms_per_step": tm["wall_s"] / steps * 1e3,
         "flops_per_step": f, "kernel_ms": kms, "kernel_tflops": f / (kms * 1e-3) / 1e12,
         "frac": f / (kms * 1e-3) / 1e12 / FP16_PEAK_TFLOPS,
+        "step_frac": f * steps / tm["step_s"] / 1e12 / FP16_PEAK_TFLOPS,
     }, out
 
 
@@ -184,10 +215,11 @@ def bench_tier(w, dev, steps, warmup):
     def step():
         doors.attention_residual_tq(res, w.q, w.k_codes, w.k_scales, w.v_codes, w.v_scales, w.q_heads, w.kv_heads,
                                     w.head_dim, w.length, w.d, w.rows, scratch)
-    wall, kms, _ = time_steps(step, steps, warmup, "tq_split")
+    tm, kms, _ = time_steps(step, steps, warmup, "tq_split")
+    ts = tm["step_s"]
     b = w.io_bytes()
     return {
-        "config": w.name, "unit": "GB/s", "value": b * steps / wall / 1e9, "ms_per_step": wall / steps * 1e3,
+        "config": w.name, "unit": "GB/s", "value": b * steps / ts / 1e9, "ms_per_step": wall / steps * 1e3,
         "bytes_per_step": b, "split_ms": kms, "kernel_gbs": b / (kms * 1e-3) / 1e9,
         "frac": b / (kms * 1e-3) / 1e9 / HBM_PEAK_GBS,
     }, res
@@ -197,13 +229,14 @@ def bench_latent(w, dev, steps, warmup):
     """Latent attention (row 137, k = v): GB/s of latents read once, q and o, and the TFLOP/s of the two
     contractions (4·heads·latent_dim a position) beside it — the shape sits near the ridge of both rooflines."""
     step, out, over = decode_setup(w, dev)
-    wall, split_ms, others = time_steps(step, steps, warmup, "decode_split")
+    tm, split_ms, others = time_steps(step, steps, warmup, "decode_split")
+    ts = tm["step_s"]
     pos = int(w.lens.astype("int64").sum())
     b = pos * w.head_dim * 2 + 2 * w.rows * w.q_heads * w.head_dim * 2
     f = 4 * w.q_heads * w.head_dim * pos
     merge_ms = others["decode_merge"][0] / max(others["decode_merge"][1], 1)
     return {
-        "config": w.name, "unit": "GB/s", "value": b * steps / wall / 1e9, "ms_per_step": wall / steps * 1e3,
+        "config": w.name, "unit": "GB/s", "value": b * steps / ts / 1e9, "ms_per_step": wall / steps * 1e3,
         "bytes_per_step": b, "flops_per_step": f, "split_ms": split_ms, "merge_ms": merge_ms,
         "kernel_gbs": b / (split_ms * 1e-3) / 1e9, "frac": b / (split_ms * 1e-3) / 1e9 / HBM_PEAK_GBS,
         "kernel_tflops": f / (split_ms * 1e-3) / 1e12,
@@ -237,16 +270,17 @@ def bench_verb(n, dev, steps, warmup):
         def step():
             verbs.rows_attention(w.q, w.k, w.v, scores, out, w.q_heads, w.kv_heads, w.head_dim, w.first, w.rows, over)
         kernel, units = "causal_mfma", w.flops()
-    wall, kms, _ = time_steps(step, steps, warmup, kernel)
+    tm, kms, _ = time_steps(step, steps, warmup, kernel)
+    ts = tm["step_s"]
     if int(over.item()):
         raise RuntimeError(f"fault word {int(over.item()):#x}")
     per_step_kernel_ms = kms   # average launch; the rows verb launches one a pass
     if n == 10:
         return {"config": "C5 through the decode verb (scores -> mix)", "unit": "GB/s",
-                "value": units * steps / wall / 1e9, "ms_per_step": wall / steps * 1e3, "bytes_per_step": units,
+                "value": units * steps / ts / 1e9, "ms_per_step": wall / steps * 1e3, "bytes_per_step": units,
                 "split_ms": per_step_kernel_ms}, out
     return {"config": "C3 through the rows verb (causal scores -> softmax -> mix, 256-row passes)", "unit": "TFLOP/s",
-            "value": units * steps / wall / 1e12, "ms_per_step": wall / steps * 1e3, "flops_per_step": units,
+            "value": units * steps / ts / 1e12, "ms_per_step": wall / steps * 1e3, "flops_per_step": units,
             "kernel_ms_per_pass": per_step_kernel_ms}, out
 
 
@@ -261,12 +295,13 @@ def bench_write(w, dev, steps, warmup):
     def step():
         doors.attention_cache_write_paged(w.k_cache, w.v_cache, w.pages, npr, w.page_size, w.capacity, w.positions,
                                           w.rows, w.k, w.v, w.cs, w.rot, w.rows, w.kv_heads, w.head_dim, over)
-    wall, kms, _ = time_steps(step, steps, warmup, "cache_write")
+    tm, kms, _ = time_steps(step, steps, warmup, "cache_write")
+    ts = tm["step_s"]
     if int(over.item()):
         raise RuntimeError(f"cache writer fault word {int(over.item()):#x}")
     b = w.io_bytes()
     return {
-        "config": w.name, "unit": "GB/s", "value": b * steps / wall / 1e9, "ms_per_step": wall / steps * 1e3,
+        "config": w.name, "unit": "GB/s", "value": b * steps / ts / 1e9, "ms_per_step": wall / steps * 1e3,
         "bytes_per_step": b, "kernel_ms": kms, "kernel_gbs": b / (kms * 1e-3) / 1e9,
         "frac": b / (kms * 1e-3) / 1e9 / HBM_PEAK_GBS,
     }, None
@@ -430,8 +465,9 @@ def main():
             secondary.append(line)
             del w
         torch.cuda.empty_cache()
-        for n in sorted([*W.TIERS, *W.WRITES, *W.LATENTS]):
-            secondary.append(isolated(n, max(5, a.steps // 2), a.warmup))
+        if a.extra:
+            for n in sorted([*W.TIERS, *W.WRITES, *W.LATENTS]):
+                secondary.append(isolated(n, max(5, a.steps // 2), a.warmup))
         if a.variants:
             secondary.append(isolated(2, a.steps, a.warmup, env={"SILVANN_GFX950_DECODE_FUSED": "1"},
                                       variant="fused finish (no merge launch)"))
@@ -446,8 +482,9 @@ def main():
                 secondary.append(isolated(n, max(5, a.steps // 2), a.warmup,
                                           env={"SILVANN_GFX950_DECODE_INLINE": "1", "SILVANN_GFX950_DECODE_FUSED": "1"},
                                           variant="one launch a step (inline plan + fused finish)"))
-        for n in (10, 11):
-            secondary.append(isolated(n, max(5, a.steps // 2), a.warmup))
+        if a.extra:
+            for n in (10, 11):
+                secondary.append(isolated(n, max(5, a.steps // 2), a.warmup))
     cpu = None if a.no_cpu else cpu_baseline(w2, a.cpu_threads)
 
     line = {
@@ -467,7 +504,8 @@ def main():
                    "q_heads": w2.q_heads, "kv_heads": w2.kv_heads, "head_dim": w2.head_dim,
                    "page_size": w2.page_size, "bytes_per_step": head["bytes_per_step"]},
         "roofline": {"bound": "hbm", "achieved": round(head["kernel_gbs"], 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(head["frac"], 4), "traffic": traffic_for("decode_split", w2.name),
+                     "frac": round(head["frac"], 4), "step_frac": round(head["step_frac"], 4),
+                     "traffic": traffic_for("decode_split", w2.name),
                      "kernel": "decode_split", "kernel_ms": round(head["split_ms"], 5),
                      "merge_ms": round(head["merge_ms"], 5)},
         "secondary": [{k: (round(v, 5) if isinstance(v, float) else v) for k, v in s.items()} for s in secondary],
