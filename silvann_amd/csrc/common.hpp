@@ -40,26 +40,51 @@ __device__ __forceinline__ float half_bits_to_float(uint16_t b) {
 // e^x as 2^(x·log2 e) on the transcendental unit; -inf gives 0.
 __device__ __forceinline__ float fast_exp(float x) { return __builtin_amdgcn_exp2f(x * kLog2e); }
 
-// Folds over the whole wave (64 lanes) and over the four 16-lane groups of a lane's column.
-__device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-    for (int s = 32; s >= 1; s >>= 1) v = fmaxf(v, __shfl_xor(v, s));
-    return v;
+// Cross-lane folds without the LDS: DPP within a row of 16 lanes (row_ror 8 and 4, then the quad
+// permutations that swap lane pairs 2 apart and 1 apart), v_permlane16_swap between rows 2k and 2k + 1 and
+// v_permlane32_swap between the wave's halves — VALU work at full rate, where __shfl_xor would be a
+// ds_bpermute through the LDS crossbar. Each step combines a lane with a partner that combines it back, with a
+// commutative operation, so every lane of the group ends with the same bits.
+template <int CTRL> __device__ __forceinline__ float dpp_mov(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
 }
-__device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-    for (int s = 32; s >= 1; s >>= 1) v += __shfl_xor(v, s);
-    return v;
+constexpr int kDppRor8 = 0x128, kDppRor4 = 0x124, kDppXor2 = 0x4E, kDppXor1 = 0xB1;
+// {lane l's value, lane l ^ 16's}, lower row first: v_permlane16_swap of a register with itself
+__device__ __forceinline__ float max_xor16(float v) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
 }
+__device__ __forceinline__ float sum_xor16(float v) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+// {lane l's value, lane l ^ 32's}, lower half first: v_permlane32_swap of a register with itself
+__device__ __forceinline__ float max_xor32(float v) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float sum_xor32(float v) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+__device__ __forceinline__ float row_max(float v) {   // over the lane's row of 16
+    v = fmaxf(v, dpp_mov<kDppRor8>(v));
+    v = fmaxf(v, dpp_mov<kDppRor4>(v));
+    v = fmaxf(v, dpp_mov<kDppXor2>(v));
+    return fmaxf(v, dpp_mov<kDppXor1>(v));
+}
+__device__ __forceinline__ float row_sum(float v) {
+    v += dpp_mov<kDppRor8>(v);
+    v += dpp_mov<kDppRor4>(v);
+    v += dpp_mov<kDppXor2>(v);
+    return v + dpp_mov<kDppXor1>(v);
+}
+// Folds over the whole wave (64 lanes; every lane active) and over the four 16-lane groups of a lane's column.
+__device__ __forceinline__ float wave_max(float v) { return max_xor32(max_xor16(row_max(v))); }
+__device__ __forceinline__ float wave_sum(float v) { return sum_xor32(sum_xor16(row_sum(v))); }
 // Over lanes l, l^16, l^32, l^48: the four row-groups of an MFMA 16x16 tile's column.
-__device__ __forceinline__ float groups_max(float v) {
-    v = fmaxf(v, __shfl_xor(v, 16));
-    return fmaxf(v, __shfl_xor(v, 32));
-}
-__device__ __forceinline__ float groups_sum(float v) {
-    v += __shfl_xor(v, 16);
-    return v + __shfl_xor(v, 32);
-}
+__device__ __forceinline__ float groups_max(float v) { return max_xor32(max_xor16(v)); }
+__device__ __forceinline__ float groups_sum(float v) { return sum_xor32(sum_xor16(v)); }
 
 // 16 bytes a lane from global memory straight into LDS: lane l's data lands at `lds` + 16·l (`lds` must be
 // the same for the whole wave). Written as its own instruction, not the builtin, so the compiler does not

@@ -292,7 +292,7 @@ __global__ __launch_bounds__(kThreads) void causal_mfma(CausalArgs a) {
             float x = sv[0];
 #pragma unroll
             for (int r = 1; r < 16; ++r) x = fmaxf(x, sv[r]);
-            x = fmaxf(x, __shfl_xor(x, 32));
+            x = max_xor32(x);
             mx = x * a.scale_log2;   // the scale is positive: max and scale commute
         };
         // Second half: the weights 2^(s·scale − m) as fp16 P^T, their row sum, P·V, and the ring's turn.
@@ -357,7 +357,7 @@ __global__ __launch_bounds__(kThreads) void causal_mfma(CausalArgs a) {
             float x = sc[0];
 #pragma unroll
             for (int r = 1; r < 16; ++r) x = fmaxf(x, sc[r]);
-            x = fmaxf(x, __shfl_xor(x, 32));
+            x = max_xor32(x);
             mx = x * a.scale_log2;
         }
         for (; t < steady_end; ++t) {
@@ -418,7 +418,7 @@ __global__ __launch_bounds__(kThreads) void causal_mfma(CausalArgs a) {
                 for (int r = 1; r < 16; ++r) x = fmaxf(x, c[r]);
             }
             sc = c;
-            x = fmaxf(x, __shfl_xor(x, 32));
+            x = max_xor32(x);
             mx = x * a.scale_log2;
             __builtin_amdgcn_s_waitcnt(0x0F70 | (2 * LOADS));   // tile t + 2 landed; tile t + 3 may fly
             __syncthreads();
@@ -430,7 +430,7 @@ __global__ __launch_bounds__(kThreads) void causal_mfma(CausalArgs a) {
             back(t);
         }
 
-        l += __shfl_xor(l, 32);
+        l = sum_xor32(l);
         if (!row_ok) return;
         if constexpr (RES) {
             // against the true max: every weight 2^(s·scale − mt) <= 1, and m in the scores' own units
@@ -548,11 +548,6 @@ __global__ __launch_bounds__(kThreads) void causal_pipe(CausalArgs a) {
             (__attribute__((address_space(3))) s16x4*)(S + vread[n % 4] + 256 * (n / 4) + (16 * s2 + 8) * RB));
         return __builtin_bit_cast(f16x8, __builtin_shufflevector(x0, x1, 0, 1, 2, 3, 4, 5, 6, 7));
     };
-    // the larger of a lane's value and its row partner's (lane ^ 32)
-    auto pair_max = [](float x) __attribute__((always_inline)) {
-        const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-        return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
-    };
 
     auto process = [&](uint32_t rtile) __attribute__((always_inline)) {
         const uint32_t wg_r0 = rtile * a.rt;
@@ -649,7 +644,7 @@ __global__ __launch_bounds__(kThreads) void causal_pipe(CausalArgs a) {
             float x = sv[0];
 #pragma unroll
             for (int r = 1; r < 16; ++r) x = fmaxf(x, sv[r]);
-            const float mx = pair_max(x) * a.scale_log2;
+            const float mx = max_xor32(x) * a.scale_log2;
             const float mnew = mx > m + kRescale ? fmaxf(m, mx) : m;
             const float c = mnew == m ? 1.0f : __builtin_amdgcn_exp2f(m - mnew);
             rescale = __builtin_amdgcn_ballot_w64(mnew != m);
@@ -728,7 +723,7 @@ __global__ __launch_bounds__(kThreads) void causal_pipe(CausalArgs a) {
                     for (int r = k * 16 / MAXS; r < (k + 1) * 16 / MAXS; ++r) x = r == 0 ? sc[0] : fmaxf(x, sc[r]);
                 }
                 if (k == MAXS) {
-                    const float mx = pair_max(x) * a.scale_log2;
+                    const float mx = max_xor32(x) * a.scale_log2;
                     mnew = mx > m + kRescale ? fmaxf(m, mx) : m;
                     cf = mnew == m ? 1.0f : __builtin_amdgcn_exp2f(m - mnew);
                     rescale = __builtin_amdgcn_ballot_w64(mnew != m);
@@ -778,7 +773,7 @@ __global__ __launch_bounds__(kThreads) void causal_pipe(CausalArgs a) {
             __syncthreads();
         }
 
-        l += __shfl_xor(l, 32);
+        l = sum_xor32(l);
         if (!row_ok) return;
         const float inv_l = 1.0f / l;
         uint16_t* orow = a.o + ((uint64_t)myrow * a.q_heads + head) * HD;

@@ -143,6 +143,29 @@ inline emu_u32x2 __builtin_amdgcn_permlane32_swap(uint32_t vdst, uint32_t src, b
         return r;
     });
 }
+inline emu_u32x2 __builtin_amdgcn_permlane16_swap(uint32_t vdst, uint32_t src, bool, bool) {
+    struct P { uint32_t d, s; };
+    const int me = emu::tl_lane;
+    return emu::wave_op(P{vdst, src}, [&](auto get) {
+        emu_u32x2 r;   // vdst's odd rows (of 16 lanes) swap with src's even rows
+        if (((me >> 4) & 1) == 0) { r[0] = get(me).d; r[1] = get(me + 16).d; }
+        else { r[0] = get(me - 16).s; r[1] = get(me).s; }
+        return r;
+    });
+}
+// DPP moves: quad_perm (ctrl < 0x100, lane i of a quad reads lane (ctrl >> 2i) & 3) and row_ror (0x121-0x12F,
+// lane i of a row of 16 reads lane (i - n) mod 16); every lane active, masks full
+inline int __builtin_amdgcn_mov_dpp(int v, int ctrl, int, int, bool) {
+    const int me = emu::tl_lane;
+    if (!(ctrl < 0x100 || (ctrl >= 0x121 && ctrl <= 0x12F))) {
+        std::fprintf(stderr, "emu: dpp control %#x\n", ctrl);
+        std::abort();
+    }
+    return emu::wave_op(v, [&](auto get) {
+        const int src = ctrl < 0x100 ? (me & ~3) | ((ctrl >> (2 * (me & 3))) & 3) : (me & ~15) | ((me - (ctrl & 15)) & 15);
+        return get(src);
+    });
+}
 #define __builtin_amdgcn_exp2f(x) exp2f(x)
 #define __builtin_amdgcn_s_waitcnt(x) emu::waitcnt(x)
 #define __builtin_amdgcn_sched_barrier(x) ((void)0)
