@@ -9,9 +9,9 @@
 //           scratch's header
 //   pass 1  decode_split: one workgroup of 4 waves a work item — (split of `chunk` positions of a row, kv
 //           head, head block of up to 16 query heads) — flattened over the rows by the plan's prefix sums,
-//           so a short row costs only its own splits and no workgroup idles (a persistent variant that
-//           takes items from the counter instead is kept behind SILVANN_GFX950_DECODE_PERSISTENT=1; it
-//           measured slower). Each wave walks
+//           so a short row costs only its own splits and no workgroup idles (one workgroup an item measured
+//           faster than a persistent grid taking items from a counter: C2 5.17 vs 4.87 TB/s, C5 6.2 vs
+//           5.1). Each wave walks
 //           32 KB tiles of K and V (32 keys at head_dim 256, 64 at 128, 128 at 64) of the split:
 //             S^T = K · Q^T     v_mfma_f32_16x16x32_f16, keys as M, the group's query heads as N (a group of
 //                               8 fills half the columns; the other half is zero — the decode is HBM-bound,
@@ -162,8 +162,7 @@ constexpr int kDefaultVariant = 2;
 
 // VARIANT bit 0: non-temporal K loads; bit 1: non-temporal value loads into LDS. GROUPED: pages shorter than
 // a tile, so each 16-key group of a tile is looked up on its own; otherwise one lookup a tile.
-// PERSISTENT: the grid is what the chip holds at once and each workgroup takes items from the counter;
-// otherwise one workgroup an item (workgroup x is item x; past the last item it returns at once).
+// One workgroup an item: workgroup x is item x; past the last item it returns at once.
 // SHARED: the keys are the values (k == v: multi-head latent attention, where one cache of latents is both,
 // engine/src/packages/ai_z__glm_5_3/cpu/opcodes/layer__abi.cuh:283-289): each tile comes into LDS once and the
 // S^T A operand is read from there. Two waves a SIMD up to head_dim 256; one at 512 (its accumulator alone is
@@ -172,11 +171,10 @@ constexpr int kDefaultVariant = 2;
 // them and writes the answers, as decode_merge does; no second launch.
 // VTR: the V^T operand read with the transposing LDS read (two a MFMA) rather than element by element (eight) —
 // at head_dim 512, where the P·V MFMAs are the most a tile has.
-template <int HD, int VARIANT, bool GROUPED, bool PERSISTENT, bool SHARED = false, bool FUSED = false, bool VTR = (HD >= 512),
+template <int HD, int VARIANT, bool GROUPED, bool SHARED = false, bool FUSED = false, bool VTR = (HD >= 512),
           bool INLINE = false>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(HD >= 512 ? 1 : 2, HD >= 512 ? 1 : 2)))
 void decode_split(DecodeArgs a) {
-    static_assert(!INLINE || !PERSISTENT, "the inline plan is for one workgroup an item");
     static_assert(!(FUSED && INLINE) || kMaxSplits < (1u << kTagShift), "a tagged count holds every split");
     constexpr int TK = tile_keys(HD);  // keys a wave takes a step: 32 KB of K and V whatever the head width
     constexpr int MT = TK / 16;      // 16-key M tiles of S^T
@@ -228,22 +226,17 @@ void decode_split(DecodeArgs a) {
         }
     }
     const uint32_t total = INLINE ? inline_total : a.plan[a.rows] * GH;
-    __shared__ uint32_t item_at;
     __shared__ uint32_t is_last;
-    // the first item is the workgroup's own index; each next one comes from the counter (which counts past
-    // the grid), asked for at the start of an item and read at its end so the atomic's trip is hidden
+    // the workgroup's item: its own index
     uint32_t item = blockIdx.x;
-    if constexpr (SHARED && !PERSISTENT) {
+    if constexpr (SHARED) {
         // XCD-aware order: workgroups go to the 8 XCDs round robin (workgroup b to XCD b % 8), and the head blocks of
         // one split read the same latents, so they take blocks 8·j + x for one x — one XCD and its L2 — and
         // consecutive j. A block past the last split gets an item past the last and returns.
         const uint32_t x = blockIdx.x & 7u, j = blockIdx.x >> 3;
         item = ((j / GH) * 8u + x) * GH + j % GH;
     }
-    for (;;) {
-    if (item >= total) break;
-    uint32_t next = 0;
-    if (PERSISTENT && threadIdx.x == 0) next = gridDim.x + atomicAdd(a.counter, 1u);
+    if (item >= total) return;
     const uint32_t sidx = item / GH, gh = item % GH;
     uint32_t lo = 0, hi = a.rows;
     if constexpr (INLINE) {
@@ -491,12 +484,6 @@ void decode_split(DecodeArgs a) {
             if (hit) *a.over = kFaultOverflow;
         }
     }
-    if (!PERSISTENT) break;
-    if (threadIdx.x == 0) item_at = next;
-    __syncthreads();   // the merge area is read before the next item's tiles land in it; item_at is written
-    item = __builtin_amdgcn_readfirstlane(item_at);   // uniform: scalar registers
-    __syncthreads();   // every wave has read item_at before thread 0 writes the next
-    }
 }
 
 // Pass 2: a workgroup of 4 or 16 waves (by the split count) per (row, query head, 64 dims). Wave w takes
@@ -717,14 +704,14 @@ void split_contiguous(const DecodeArgs& a, uint64_t head_dim, bool shared, uint6
     const uint64_t gh = (uint64_t)a.kv_heads * a.hblocks;
     const dim3 grid((uint32_t)(splits * gh));
     if (head_dim == 512) {
-        if (shared) decode_split<512, 2, false, false, true, false, true, INL><<<dim3(shared_grid(splits, gh)), kThreads, 0, st>>>(a);
-        else decode_split<512, 2, false, false, false, false, true, INL><<<grid, kThreads, 0, st>>>(a);
+        if (shared) decode_split<512, 2, false, true, false, true, INL><<<dim3(shared_grid(splits, gh)), kThreads, 0, st>>>(a);
+        else decode_split<512, 2, false, false, false, true, INL><<<grid, kThreads, 0, st>>>(a);
     } else if (head_dim == 256) {
-        decode_split<256, kDefaultVariant, false, false, false, false, false, INL><<<grid, kThreads, 0, st>>>(a);
+        decode_split<256, kDefaultVariant, false, false, false, false, INL><<<grid, kThreads, 0, st>>>(a);
     } else if (head_dim == 128) {
-        decode_split<128, kDefaultVariant, false, false, false, false, false, INL><<<grid, kThreads, 0, st>>>(a);
+        decode_split<128, kDefaultVariant, false, false, false, false, INL><<<grid, kThreads, 0, st>>>(a);
     } else {
-        decode_split<64, kDefaultVariant, false, false, false, false, false, INL><<<grid, kThreads, 0, st>>>(a);
+        decode_split<64, kDefaultVariant, false, false, false, false, INL><<<grid, kThreads, 0, st>>>(a);
     }
 }
 
@@ -787,55 +774,47 @@ void decode_paged_launch(uint16_t* o, const uint16_t* q, const uint16_t* k, cons
         refuse("attention_decode_paged");
         return;
     }
-    const dim3 pgrid((uint32_t)(items < resident_groups() ? items : resident_groups()));
     const dim3 igrid((uint32_t)items);
-    static const int mode = [] {
-        const char* e = getenv("SILVANN_GFX950_DECODE_PERSISTENT");
-        return e ? (int)strtol(e, nullptr, 10) : -1;
-    }();
-    // measured: one workgroup an item beats the queue at both benchmark shapes (C2 5.17 vs 4.87 TB/s,
-    // C5 6.2 vs 5.1), so the queue is opt-in
-    const bool persistent = mode > 0;
     const bool fused = fused_finish();
-    if (fused && head_dim <= 256 && !persistent && inline_plan() && rows <= 64) {
+    if (fused && head_dim <= 256 && inline_plan() && rows <= 64) {
         // one launch: the plan made in the kernel, the counts tagged with this call's tag
         a.tag = next_tag();
         prof_begin(kProfDecodeSplit);
         const uint32_t hv = (uint32_t)head_dim;
         if (grouped) {
-            if (hv == 64) decode_split<64, kDefaultVariant, true, false, false, true, false, true><<<igrid, kThreads, 0, st>>>(a);
-            else if (hv == 128) decode_split<128, kDefaultVariant, true, false, false, true, false, true><<<igrid, kThreads, 0, st>>>(a);
-            else decode_split<256, kDefaultVariant, true, false, false, true, false, true><<<igrid, kThreads, 0, st>>>(a);
+            if (hv == 64) decode_split<64, kDefaultVariant, true, false, true, false, true><<<igrid, kThreads, 0, st>>>(a);
+            else if (hv == 128) decode_split<128, kDefaultVariant, true, false, true, false, true><<<igrid, kThreads, 0, st>>>(a);
+            else decode_split<256, kDefaultVariant, true, false, true, false, true><<<igrid, kThreads, 0, st>>>(a);
         } else {
-            if (hv == 64) decode_split<64, kDefaultVariant, false, false, false, true, false, true><<<igrid, kThreads, 0, st>>>(a);
-            else if (hv == 128) decode_split<128, kDefaultVariant, false, false, false, true, false, true><<<igrid, kThreads, 0, st>>>(a);
-            else decode_split<256, kDefaultVariant, false, false, false, true, false, true><<<igrid, kThreads, 0, st>>>(a);
+            if (hv == 64) decode_split<64, kDefaultVariant, false, false, true, false, true><<<igrid, kThreads, 0, st>>>(a);
+            else if (hv == 128) decode_split<128, kDefaultVariant, false, false, true, false, true><<<igrid, kThreads, 0, st>>>(a);
+            else decode_split<256, kDefaultVariant, false, false, true, false, true><<<igrid, kThreads, 0, st>>>(a);
         }
         prof_end(kProfDecodeSplit);
         check_launch("attention_decode_paged");
         return;
     }
-    if (fused && head_dim <= 256 && !persistent) {
+    if (fused && head_dim <= 256) {
         const uint32_t units = a.kv_heads * a.hblocks;
         decode_plan<true><<<1, 256, 0, st>>>(lens, a.rows, a.chunk, (uint32_t*)a.plan, a.counter, a.done, units, o,
                                              a.q_heads * (uint32_t)head_dim);
         prof_begin(kProfDecodeSplit);
         const uint32_t hv = (uint32_t)head_dim;
         if (grouped) {
-            if (hv == 64) decode_split<64, kDefaultVariant, true, false, false, true><<<igrid, kThreads, 0, st>>>(a);
-            else if (hv == 128) decode_split<128, kDefaultVariant, true, false, false, true><<<igrid, kThreads, 0, st>>>(a);
-            else decode_split<256, kDefaultVariant, true, false, false, true><<<igrid, kThreads, 0, st>>>(a);
+            if (hv == 64) decode_split<64, kDefaultVariant, true, false, true><<<igrid, kThreads, 0, st>>>(a);
+            else if (hv == 128) decode_split<128, kDefaultVariant, true, false, true><<<igrid, kThreads, 0, st>>>(a);
+            else decode_split<256, kDefaultVariant, true, false, true><<<igrid, kThreads, 0, st>>>(a);
         } else {
-            if (hv == 64) decode_split<64, kDefaultVariant, false, false, false, true><<<igrid, kThreads, 0, st>>>(a);
-            else if (hv == 128) decode_split<128, kDefaultVariant, false, false, false, true><<<igrid, kThreads, 0, st>>>(a);
-            else decode_split<256, kDefaultVariant, false, false, false, true><<<igrid, kThreads, 0, st>>>(a);
+            if (hv == 64) decode_split<64, kDefaultVariant, false, false, true><<<igrid, kThreads, 0, st>>>(a);
+            else if (hv == 128) decode_split<128, kDefaultVariant, false, false, true><<<igrid, kThreads, 0, st>>>(a);
+            else decode_split<256, kDefaultVariant, false, false, true><<<igrid, kThreads, 0, st>>>(a);
         }
         prof_end(kProfDecodeSplit);
         check_launch("attention_decode_paged");
         return;
     }
     // the plan made inside decode_split at batches of at most 64 rows: one launch fewer a step
-    const bool inlined = inline_plan() && rows <= 64 && head_dim <= 256 && !persistent && !vtr();
+    const bool inlined = inline_plan() && rows <= 64 && head_dim <= 256 && !vtr();
     if (!inlined) decode_plan<<<1, 256, 0, st>>>(lens, a.rows, a.chunk, (uint32_t*)a.plan, a.counter);
     prof_begin(kProfDecodeSplit);
     // head_dim 512: one workgroup an item; the shared-tile form when the keys are the values
@@ -843,31 +822,31 @@ void decode_paged_launch(uint16_t* o, const uint16_t* q, const uint16_t* k, cons
     if (head_dim == 512) {
         if (shared) {
             const dim3 sgrid(shared_grid(rows * a.nsplit, kv_heads * a.hblocks));
-            if (grouped) decode_split<512, 2, true, false, true><<<sgrid, kThreads, 0, st>>>(a);
-            else decode_split<512, 2, false, false, true><<<sgrid, kThreads, 0, st>>>(a);
+            if (grouped) decode_split<512, 2, true, true><<<sgrid, kThreads, 0, st>>>(a);
+            else decode_split<512, 2, false, true><<<sgrid, kThreads, 0, st>>>(a);
         } else {
-            if (grouped) decode_split<512, 2, true, false><<<igrid, kThreads, 0, st>>>(a);
-            else decode_split<512, 2, false, false><<<igrid, kThreads, 0, st>>>(a);
+            if (grouped) decode_split<512, 2, true><<<igrid, kThreads, 0, st>>>(a);
+            else decode_split<512, 2, false><<<igrid, kThreads, 0, st>>>(a);
         }
     } else if (inlined) {
         switch (head_dim) {
 #define SILVANN_DECODE_INLINE(HDV) \
             case HDV: \
-                if (grouped) decode_split<HDV, kDefaultVariant, true, false, false, false, false, true><<<igrid, kThreads, 0, st>>>(a); \
-                else decode_split<HDV, kDefaultVariant, false, false, false, false, false, true><<<igrid, kThreads, 0, st>>>(a); \
+                if (grouped) decode_split<HDV, kDefaultVariant, true, false, false, false, true><<<igrid, kThreads, 0, st>>>(a); \
+                else decode_split<HDV, kDefaultVariant, false, false, false, false, true><<<igrid, kThreads, 0, st>>>(a); \
                 break;
             SILVANN_DECODE_INLINE(64) SILVANN_DECODE_INLINE(128) SILVANN_DECODE_INLINE(256)
 #undef SILVANN_DECODE_INLINE
             default: break;
         }
-    } else if (vtr() && !persistent) {
+    } else if (vtr()) {
         // the transposing V^T read at head_dim <= 256 (SILVANN_GFX950_DECODE_VTR=1): checked in the CPU emulation,
         // not yet measured against the element reads these widths run by default
         switch (head_dim) {
 #define SILVANN_DECODE_VTR(HDV) \
             case HDV: \
-                if (grouped) decode_split<HDV, kDefaultVariant, true, false, false, false, true><<<igrid, kThreads, 0, st>>>(a); \
-                else decode_split<HDV, kDefaultVariant, false, false, false, false, true><<<igrid, kThreads, 0, st>>>(a); \
+                if (grouped) decode_split<HDV, kDefaultVariant, true, false, false, true><<<igrid, kThreads, 0, st>>>(a); \
+                else decode_split<HDV, kDefaultVariant, false, false, false, true><<<igrid, kThreads, 0, st>>>(a); \
                 break;
             SILVANN_DECODE_VTR(64) SILVANN_DECODE_VTR(128) SILVANN_DECODE_VTR(256)
 #undef SILVANN_DECODE_VTR
@@ -876,13 +855,8 @@ void decode_paged_launch(uint16_t* o, const uint16_t* q, const uint16_t* k, cons
     } else switch (head_dim * 4 + variant) {
 #define SILVANN_DECODE_CASE(HDV, VAR) \
         case HDV * 4 + VAR: \
-            if (persistent) { \
-                if (grouped) decode_split<HDV, VAR, true, true><<<pgrid, kThreads, 0, st>>>(a); \
-                else decode_split<HDV, VAR, false, true><<<pgrid, kThreads, 0, st>>>(a); \
-            } else { \
-                if (grouped) decode_split<HDV, VAR, true, false><<<igrid, kThreads, 0, st>>>(a); \
-                else decode_split<HDV, VAR, false, false><<<igrid, kThreads, 0, st>>>(a); \
-            } \
+            if (grouped) decode_split<HDV, VAR, true><<<igrid, kThreads, 0, st>>>(a); \
+            else decode_split<HDV, VAR, false><<<igrid, kThreads, 0, st>>>(a); \
             break;
         SILVANN_DECODE_CASE(64, 0) SILVANN_DECODE_CASE(64, 1) SILVANN_DECODE_CASE(64, 2) SILVANN_DECODE_CASE(64, 3)
         SILVANN_DECODE_CASE(128, 0) SILVANN_DECODE_CASE(128, 1) SILVANN_DECODE_CASE(128, 2) SILVANN_DECODE_CASE(128, 3)
@@ -954,9 +928,9 @@ bool decode_one(uint16_t* o, float* res, const uint16_t* q, const uint16_t* k, c
         a.lens_out = lens;
         a.tag = next_tag();
         const dim3 grid((uint32_t)(nsplit * kv_heads * hblocks));
-        if (head_dim == 256) decode_split<256, kDefaultVariant, false, false, false, true, false, true><<<grid, kThreads, 0, st>>>(a);
-        else if (head_dim == 128) decode_split<128, kDefaultVariant, false, false, false, true, false, true><<<grid, kThreads, 0, st>>>(a);
-        else decode_split<64, kDefaultVariant, false, false, false, true, false, true><<<grid, kThreads, 0, st>>>(a);
+        if (head_dim == 256) decode_split<256, kDefaultVariant, false, false, true, false, true><<<grid, kThreads, 0, st>>>(a);
+        else if (head_dim == 128) decode_split<128, kDefaultVariant, false, false, true, false, true><<<grid, kThreads, 0, st>>>(a);
+        else decode_split<64, kDefaultVariant, false, false, true, false, true><<<grid, kThreads, 0, st>>>(a);
         prof_end(kProfDecodeSplit);
         return true;
     }
