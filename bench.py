@@ -8,7 +8,7 @@ tables — through the split-K decode door (silvann_gfx950_attention_decode_page
 the whole batch; `value` is its algorithmic bytes (each cached K and V row once, plus q, o and the page
 table entries) × K over the K steps' own durations, inputs resident in HBM. Before each timed step a 1 GiB
 buffer is written, so no step finds its inputs in the 256 MB Infinity Cache or the L2s; each step is bracketed
-by hipEvents on the null stream, the one the library launches on, and the flushes fall outside them
+by hipEvents on the stream the library launches on, and the flushes fall outside them
 (`wall_ms_per_step` in the lines is the wall clock of the whole timed region, flushes included).
 
 `roofline` is the dominant kernel's (decode_split): algorithmic bytes ÷ its average launch duration, timed
@@ -102,12 +102,14 @@ def _flush_l2():
 
 def time_steps(step, steps, warmup, kernel):
     """Warm up, then time exactly `steps` steps, each after a cache flush: the steps' own durations (hipEvents on
-    the stream the library launches on, around each step, the flush outside them), the wall clock of the whole
+    torch's current stream, which the library is set to launch on, around each step, the flush outside them), the wall clock of the whole
     timed region between device synchronisations (flushes included), and the named kernel's average launch
     duration (the library's hipEvents around that kernel)."""
     import torch
     import silvann_amd
     L = silvann_amd.lib()
+    stream = torch.cuda.current_stream()
+    silvann_amd.doors.set_stream(stream)   # the library's launches, the flushes and the events on one stream
     for _ in range(warmup):
         step()
     torch.cuda.synchronize()
@@ -115,8 +117,6 @@ def time_steps(step, steps, warmup, kernel):
     for k in KERNELS:
         prof_read(k)
     evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
-    stream = torch.cuda.current_stream()
-    assert stream.cuda_stream == 0, "the library launches on the null stream; time it there"
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for a, b in evs:
