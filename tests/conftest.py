@@ -19,6 +19,40 @@ def pytest_configure(config):
 GPU_FIRST = ("test_gpu_decode.py", "test_gpu_doors.py", "test_gpu_prefill.py")
 
 
+_current = {"test": "(collecting)"}
+
+
+def pytest_sessionstart(session):
+    """Under `-m gpu`: a heartbeat file, gpurun_out/pytest_heartbeat.txt, rewritten every 20 s with the running test
+    and its time so far, so a long test (a child-process suite, whose output pytest holds until it ends) shows
+    progress to a run that watches for silence."""
+    if (session.config.option.markexpr or "").strip() != "gpu":
+        return
+    import threading
+    import time
+    out = ROOT / "gpurun_out"
+
+    def beat():
+        t0, last = time.time(), None
+        while True:
+            test = _current["test"]
+            if test != last:
+                t_test, last = time.time(), test
+            try:
+                out.mkdir(exist_ok=True)
+                (out / "pytest_heartbeat.txt").write_text(
+                    f"{time.time() - t0:.0f} s into the session; {test} for {time.time() - t_test:.0f} s\n")
+            except OSError:
+                return
+            time.sleep(20)
+
+    threading.Thread(target=beat, daemon=True, name="pytest-heartbeat").start()
+
+
+def pytest_runtest_logstart(nodeid, location):
+    _current["test"] = nodeid
+
+
 def pytest_collection_modifyitems(config, items):
     def rank(item):
         name = Path(str(item.fspath)).name
