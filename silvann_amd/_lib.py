@@ -6,6 +6,7 @@ missing extension is an error, never a silent CPU path.
 from __future__ import annotations
 
 import ctypes as C
+import os
 import re
 from pathlib import Path
 
@@ -84,13 +85,16 @@ def header_functions() -> list[str]:
 
 
 def lib() -> C.CDLL:
+    """The library, loaded once a process: LIB_PATH, or the build SILVANN_GFX950_LIB names (an experiment build of
+    the same sources)."""
     global _LIB
     if _LIB is not None:
         return _LIB
-    if not LIB_PATH.exists():
-        raise LibraryMissing(f"{LIB_PATH} is not built: run `python -c 'import __graft_entry__ as g; g.build()'` "
+    path = Path(os.environ.get("SILVANN_GFX950_LIB") or LIB_PATH)
+    if not path.exists():
+        raise LibraryMissing(f"{path} is not built: run `python -c 'import __graft_entry__ as g; g.build()'` "
                              "or `python silvann_amd/build.py`")
-    L = C.CDLL(str(LIB_PATH))
+    L = C.CDLL(str(path))
     for name, args in SIGNATURES.items():
         fn = getattr(L, name)
         fn.argtypes = args

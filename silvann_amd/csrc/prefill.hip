@@ -35,6 +35,13 @@
 namespace silvann {
 namespace {
 
+#ifndef SILVANN_PREFILL_KA
+#define SILVANN_PREFILL_KA 4
+#endif
+#ifndef SILVANN_PREFILL_VA
+#define SILVANN_PREFILL_VA 2
+#endif
+
 constexpr int kKT = 32;      // keys a tile
 constexpr int kWaves = 4;
 constexpr int kThreads = 64 * kWaves;
@@ -376,7 +383,10 @@ __global__ __launch_bounds__(kThreads) void causal_mfma(CausalArgs a) {
                     (__attribute__((address_space(3))) s16x4*)(SV + vread[n % 4] + 256 * (n / 4) + (16 * s2 + 8) * RB));
                 return __builtin_bit_cast(f16x8, __builtin_shufflevector(x0, x1, 0, 1, 2, 3, 4, 5, 6, 7));
             };
-            constexpr int KA = 4, VA = 2;   // operand reads ahead of their MFMA
+            // operand reads ahead of their MFMA (K operands KA MFMAs ahead, V^T operands VA; experiment builds set
+            // them with -D, the defaults are the measured choice)
+            constexpr int KA = SILVANN_PREFILL_KA, VA = SILVANN_PREFILL_VA;
+            static_assert(VA >= 1 && VA <= KA && KA + 1 <= KSTEPS, "V reads take the last K-read slots");
             f16x8 kb[KA + 1], vb[VA + 2];
             f32x16 c = (f32x16)0.0f;
             float lsum = 0.0f;
@@ -389,8 +399,8 @@ __global__ __launch_bounds__(kThreads) void causal_mfma(CausalArgs a) {
             for (int kk = 0; kk < KSTEPS; ++kk) {
                 c = __builtin_amdgcn_mfma_f32_32x32x16_f16(kb[kk % (KA + 1)], qb[kk], c, 0, 0, 0);
                 if (kk + KA < KSTEPS) kb[(kk + KA) % (KA + 1)] = kread_at(kk + KA);
-                if (kk + KA == KSTEPS) vb[0] = vread_at(0);
-                if (kk + KA == KSTEPS + 1) vb[1] = vread_at(1);
+                // the S^T loop's last KA steps read no K: their slots bring the first VA V^T operands
+                if (kk + KA >= KSTEPS && kk + KA - KSTEPS < VA) vb[kk + KA - KSTEPS] = vread_at(kk + KA - KSTEPS);
                 // the weights of tile t, spread over the MFMAs (one each when KSTEPS is 16)
 #pragma unroll
                 for (int r = kk * 16 / KSTEPS; r < (kk + 1) * 16 / KSTEPS; ++r) {
@@ -400,7 +410,6 @@ __global__ __launch_bounds__(kThreads) void causal_mfma(CausalArgs a) {
                 }
                 __builtin_amdgcn_sched_barrier(0);
             }
-            if (KSTEPS < KA + 1) { vb[0] = vread_at(0); vb[1] = vread_at(1); }
             l += lsum;
             float x = 0.0f;
 #pragma unroll
