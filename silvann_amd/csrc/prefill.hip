@@ -41,6 +41,9 @@ namespace {
 #ifndef SILVANN_PREFILL_VA
 #define SILVANN_PREFILL_VA 2
 #endif
+#ifndef SILVANN_PREFILL_XCD_ORDER   // 0: workgroups in launch order (an experiment build's comparison)
+#define SILVANN_PREFILL_XCD_ORDER 1
+#endif
 
 constexpr int kKT = 32;      // keys a tile
 constexpr int kWaves = 4;
@@ -119,6 +122,17 @@ __device__ __forceinline__ void scale_acc(float& x, float c) {
                  : "v"(c));
 }
 
+// XCD-aware workgroup order. The hardware deals a launch's workgroups to the 8 XCDs round robin (linear id % 8),
+// and each XCD has its own L2. The logical index M = (id % 8)·(N / 8) + id / 8 gives each XCD a contiguous range
+// of logical workgroups, which run x-fastest: the row tiles of one head block, so the K/V tiles they all stream
+// are fetched into one XCD's L2 instead of every XCD's. A bijection when N is a multiple of 8 (else the identity).
+struct Block { uint32_t x, y; };
+__device__ __forceinline__ Block xcd_block() {
+    const uint32_t n = gridDim.x * gridDim.y, id = blockIdx.x + blockIdx.y * gridDim.x;
+    const uint32_t m = SILVANN_PREFILL_XCD_ORDER && n % 8 == 0 ? (id % 8) * (n / 8) + id / 8 : id;
+    return {m % gridDim.x, m / gridDim.x};
+}
+
 // PTL: the page table fits LDS (kPagesInLds entries) and tiles look their page up there.
 // RES: write each row's residual {m, l, acc} (the reference's `attention_weights` + `attention_residual_mix`
 // contract, kernels.cuh:1186-1238: m the row's largest scaled score, l = Σ e^(s − m), acc = Σ e^(s − m)·v)
@@ -135,7 +149,8 @@ __global__ __launch_bounds__(kThreads) void causal_mfma(CausalArgs a) {
 
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
     const int col = lane & 31, half = lane >> 5;
-    const uint32_t g = blockIdx.y / a.hblocks, hb = blockIdx.y % a.hblocks;
+    const Block blk = xcd_block();
+    const uint32_t g = blk.y / a.hblocks, hb = blk.y % a.hblocks;
     const uint32_t head = g * a.group + hb * a.hw + (w % a.hw);
     const uint32_t row = a.kv_heads * HD;   // elements a cache position
     bool hit = false;
@@ -474,11 +489,11 @@ __global__ __launch_bounds__(kThreads) void causal_mfma(CausalArgs a) {
 
     if (PAIRED) {
         // row tiles N-1-x (heavy) then x (light): the same work for every workgroup
-        const uint32_t heavy = a.rtiles - 1 - blockIdx.x, light = blockIdx.x;
+        const uint32_t heavy = a.rtiles - 1 - blk.x, light = blk.x;
         process(heavy);
         if (light < heavy) process(light);
     } else {
-        process(a.rtiles - 1 - blockIdx.x);   // heaviest first
+        process(a.rtiles - 1 - blk.x);   // heaviest first
     }
     if (hit) *a.over = kFaultOverflow;
 }

@@ -33,6 +33,7 @@ def _causal(oracle, hd, qh, kvh, first, rows, ps, env=None):
 @pytest.mark.parametrize("hd,qh,kvh,first,rows,ps", [
     (128, 6, 2, 10, 70, 0),      # group 3: one head a wave, waves on different rows
     (256, 16, 2, 77, 95, 64),    # paged, page table in LDS, the steady loop at head_dim 256
+    (64, 8, 1, 300, 256, 32),    # 8 workgroups of 8 row tiles: the XCD-aware order permutes them
 ])
 def test_causal_default_kernel(oracle, hd, qh, kvh, first, rows, ps):
     _causal(oracle, hd, qh, kvh, first, rows, ps)
