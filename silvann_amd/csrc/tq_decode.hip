@@ -72,7 +72,7 @@ template <int D> __device__ __forceinline__ f16x8 decode8(uint64_t bits, float s
 }
 
 template <int HD, int D>
-__global__ __launch_bounds__(kThreads) void tq_split(TqArgs a) {
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))) void tq_split(TqArgs a) {
     constexpr int TK = tile_keys(HD);
     constexpr int MT = TK / 16;       // 16-key M tiles of S^T
     constexpr int KS = HD / 32;       // k-steps of S^T
@@ -120,16 +120,19 @@ __global__ __launch_bounds__(kThreads) void tq_split(TqArgs a) {
     for (uint32_t j = w; j < ntiles; j += kWaves) {
         const uint32_t t0 = start + j * TK;
         const uint32_t nvalid = min((uint32_t)TK, end - t0);
-        // K as the A operand; keys past the split read key t0 (their scores are masked)
-        f16x8 kr[MT][KS];
+        // K codes as the A operand's source; keys past the split read key t0 (their scores are masked). The codes
+        // are held raw (a 32- or 64-bit word a k-step) and decoded one 16-key M tile at a time, just before its
+        // MFMAs, so the decoded fp16 operands of only one M tile are live at once.
+        uint64_t kcodes[MT][KS];
+        float kscale[MT];
 #pragma unroll
         for (int p = 0; p < MT; ++p) {
             const int key = 16 * p + col;
             const uint64_t krow = (uint64_t)(t0 + (key < (int)nvalid ? key : 0)) * a.kv_heads + g;
             const uint8_t* row = a.kc + krow * rb;
-            const float sc = half_bits_to_float(a.ks[krow]);
+            kscale[p] = half_bits_to_float(a.ks[krow]);
 #pragma unroll
-            for (int ks = 0; ks < KS; ++ks) kr[p][ks] = decode8<D>(codes8<D>(row, 32 * ks + 8 * grp), sc, lev);
+            for (int ks = 0; ks < KS; ++ks) kcodes[p][ks] = codes8<D>(row, 32 * ks + 8 * grp);
         }
         // V decoded into the wave's tile: slot (key, c) holds chunk c ^ f(key) of the key's row; keys past the
         // split bring key t0 (weight 0)
@@ -146,7 +149,8 @@ __global__ __launch_bounds__(kThreads) void tq_split(TqArgs a) {
         for (int p = 0; p < MT; ++p) {
             f32x4 st = (f32x4)0.0f;
 #pragma unroll
-            for (int ks = 0; ks < KS; ++ks) st = __builtin_amdgcn_mfma_f32_16x16x32_f16(kr[p][ks], qb[ks], st, 0, 0, 0);
+            for (int ks = 0; ks < KS; ++ks)
+                st = __builtin_amdgcn_mfma_f32_16x16x32_f16(decode8<D>(kcodes[p][ks], kscale[p], lev), qb[ks], st, 0, 0, 0);
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
                 const int key = 16 * p + 4 * grp + r;
@@ -272,7 +276,7 @@ uint32_t tq_hblocks(uint64_t q_heads, uint64_t kv_heads) { return (uint32_t)((q_
 
 bool tq_shape_ok(uint64_t q_heads, uint64_t kv_heads, uint64_t head_dim, uint64_t length, uint64_t d, uint64_t rows) {
     return (head_dim == 64 || head_dim == 128 || head_dim == 256) && (d == 4 || d == 8) && kv_heads > 0 &&
-           q_heads % kv_heads == 0 && length < (1ull << 31) && rows > 0 && rows <= 65535 &&
+           q_heads > 0 && q_heads % kv_heads == 0 && length < (1ull << 31) && rows > 0 && rows <= 65535 &&
            kv_heads * tq_hblocks(q_heads, kv_heads) <= 65535;
 }
 
