@@ -17,6 +17,9 @@ def pytest_configure(config):
 # GPU suites whose kernels have passed on an MI355X run first, so that under `pytest -x` a failure in a newer suite
 # cannot hide their results; the rest keep their collection order after them.
 GPU_FIRST = ("test_gpu_decode.py", "test_gpu_doors.py", "test_gpu_prefill.py")
+# The opt-in variants of the decode (candidates for its default, not paths a caller gets) run after every suite of
+# a path a caller gets, so that a failure among them cannot hide those suites' results either.
+GPU_LAST = ("test_gpu_decode_variants.py",)
 
 
 _current = {"test": "(collecting)"}
@@ -56,7 +59,9 @@ def pytest_runtest_logstart(nodeid, location):
 def pytest_collection_modifyitems(config, items):
     def rank(item):
         name = Path(str(item.fspath)).name
-        return GPU_FIRST.index(name) if name in GPU_FIRST else len(GPU_FIRST)
+        if name in GPU_FIRST:
+            return GPU_FIRST.index(name)
+        return len(GPU_FIRST) + (1 + GPU_LAST.index(name) if name in GPU_LAST else 0)
     items[:] = sorted(items, key=rank)
 
 
