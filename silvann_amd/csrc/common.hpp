@@ -40,24 +40,22 @@ __device__ __forceinline__ float half_bits_to_float(uint16_t b) {
 // e^x as 2^(x·log2 e) on the transcendental unit; -inf gives 0.
 __device__ __forceinline__ float fast_exp(float x) { return __builtin_amdgcn_exp2f(x * kLog2e); }
 
-// Cross-lane folds without the LDS: DPP within a row of 16 lanes (row_ror 8 and 4, then the quad
-// permutations that swap lane pairs 2 apart and 1 apart), v_permlane16_swap between rows 2k and 2k + 1 and
-// v_permlane32_swap between the wave's halves — VALU work at full rate, where __shfl_xor would be a
-// ds_bpermute through the LDS crossbar. Each step combines a lane with a partner that combines it back, with a
-// commutative operation, so every lane of the group ends with the same bits.
+// Cross-lane folds: DPP within a row of 16 lanes (row_ror 8 and 4, then the quad permutations that swap lane
+// pairs 2 apart and 1 apart), ds_swizzle in its bitmask mode for lane ^ 16 (no LDS bank access), and
+// v_permlane32_swap between the wave's halves — where __shfl_xor would be a ds_bpermute a step. Each step combines
+// a lane with a partner that combines it back, with a commutative operation, so every lane of the group ends with
+// the same bits.
 template <int CTRL> __device__ __forceinline__ float dpp_mov(float v) {
     return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
 }
 constexpr int kDppRor8 = 0x128, kDppRor4 = 0x124, kDppXor2 = 0x4E, kDppXor1 = 0xB1;
-// {lane l's value, lane l ^ 16's}, lower row first: v_permlane16_swap of a register with itself
-__device__ __forceinline__ float max_xor16(float v) {
-    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
-    return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+// ds_swizzle offset, bitmask mode (bit 15 clear): and_mask 0x1F, or_mask 0, xor_mask 0x10 — lane l reads l ^ 16
+constexpr int kSwizzleXor16 = 0x401F;
+__device__ __forceinline__ float xor16(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, v), kSwizzleXor16));
 }
-__device__ __forceinline__ float sum_xor16(float v) {
-    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
-    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
-}
+__device__ __forceinline__ float max_xor16(float v) { return fmaxf(v, xor16(v)); }
+__device__ __forceinline__ float sum_xor16(float v) { return v + xor16(v); }
 // {lane l's value, lane l ^ 32's}, lower half first: v_permlane32_swap of a register with itself
 __device__ __forceinline__ float max_xor32(float v) {
     const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);

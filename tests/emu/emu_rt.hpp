@@ -143,15 +143,15 @@ inline emu_u32x2 __builtin_amdgcn_permlane32_swap(uint32_t vdst, uint32_t src, b
         return r;
     });
 }
-inline emu_u32x2 __builtin_amdgcn_permlane16_swap(uint32_t vdst, uint32_t src, bool, bool) {
-    struct P { uint32_t d, s; };
+// ds_swizzle, bitmask mode only (offset bit 15 clear): lane l of each 32 reads ((l & and) | or) ^ xor
+inline int __builtin_amdgcn_ds_swizzle(int v, int offset) {
     const int me = emu::tl_lane;
-    return emu::wave_op(P{vdst, src}, [&](auto get) {
-        emu_u32x2 r;   // vdst's odd rows (of 16 lanes) swap with src's even rows
-        if (((me >> 4) & 1) == 0) { r[0] = get(me).d; r[1] = get(me + 16).d; }
-        else { r[0] = get(me - 16).s; r[1] = get(me).s; }
-        return r;
-    });
+    if (offset & 0x8000) {
+        std::fprintf(stderr, "emu: ds_swizzle offset %#x\n", offset);
+        std::abort();
+    }
+    const int andm = offset & 31, orm = (offset >> 5) & 31, xorm = (offset >> 10) & 31;
+    return emu::wave_op(v, [&](auto get) { return get((me & ~31) | ((((me & 31) & andm) | orm) ^ xorm)); });
 }
 // DPP moves: quad_perm (ctrl < 0x100, lane i of a quad reads lane (ctrl >> 2i) & 3) and row_ror (0x121-0x12F,
 // lane i of a row of 16 reads lane (i - n) mod 16); every lane active, masks full
