@@ -111,6 +111,7 @@ def time_steps(step, steps, warmup, kernel):
     stream = torch.cuda.current_stream()
     silvann_amd.doors.set_stream(stream)   # the library's launches, the flushes and the events on one stream
     for _ in range(warmup):
+        _flush_l2()   # the flush buffer is allocated here, before any timing
         step()
     torch.cuda.synchronize()
     L.silvann_gfx950_profile_enable(1)
