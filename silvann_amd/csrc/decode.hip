@@ -668,7 +668,11 @@ bool vtr() {
     return on;
 }
 
-// The fused finish (SILVANN_GFX950_DECODE_FUSED=1): checked in the CPU emulation, not yet measured on a GPU.
+// The fused finish (SILVANN_GFX950_DECODE_FUSED=1): checked in the CPU emulation, not yet measured on a GPU. It is
+// taken only for rows of at most kFusedMaxSplits splits: its one finishing workgroup a (row, kv head, head block)
+// reads every split's residual alone — at C5's 256 splits of 8 heads × 258 floats, 2.1 MB through one CU — where
+// decode_merge spreads that over a workgroup a (head, 64 dims).
+constexpr uint32_t kFusedMaxSplits = 32;
 bool fused_finish() {
     static const bool on = [] {
         const char* e = getenv("SILVANN_GFX950_DECODE_FUSED");
@@ -775,7 +779,7 @@ void decode_paged_launch(uint16_t* o, const uint16_t* q, const uint16_t* k, cons
         return;
     }
     const dim3 igrid((uint32_t)items);
-    const bool fused = fused_finish();
+    const bool fused = fused_finish() && a.nsplit <= kFusedMaxSplits;
     if (fused && head_dim <= 256 && inline_plan() && rows <= 64) {
         // one launch: the plan made in the kernel, the counts tagged with this call's tag
         a.tag = next_tag();
@@ -921,7 +925,7 @@ bool decode_one(uint16_t* o, float* res, const uint16_t* q, const uint16_t* k, c
     a.tag = 0;
     hipStream_t st = stream();
     prof_begin(kProfDecodeSplit);
-    if (o && !sink && head_dim <= 256 && inline_plan() && fused_finish()) {
+    if (o && !sink && head_dim <= 256 && inline_plan() && fused_finish() && nsplit <= kFusedMaxSplits) {
         // one launch: the last split of each head block finishes the answers, its counts tagged
         a.lens = nullptr;
         a.len_first = (uint32_t)length;

@@ -171,3 +171,16 @@ def test_decode_one_launch(oracle, qh, kvh, hd, lens, ps, repeat):
     assert over == 0
     launched = [ln for ln in log.splitlines() if ln.startswith("emu launch ")]
     assert len(launched) == 1 + repeat and all("decode_split" in x for x in launched), launched
+
+
+def test_decode_long_rows_keep_the_merge_launch(oracle):
+    """With the fused finish and the inline plan switched on, a row of more than 32 splits (here 40) keeps the
+    merge launch: one finishing workgroup would read every split's residual alone. The answers are the oracle's."""
+    w = W.decode("emu", 4, 4, 64, [20000, 300], page_size=0, seed=77)
+    got, over, log = emu.run_decode(w, env={**FUSED, **INLINE})
+    want, _ = oracle.decode_paged(w.q, w.k, w.v, w.pages, w.pages_row, w.page_size, w.k_row, w.lens, 4, 4, 64,
+                                  w.rows)
+    parity(got, want)
+    assert over == 0
+    launched = [ln for ln in log.splitlines() if ln.startswith("emu launch ")]
+    assert len(launched) == 2 and "decode_split" in launched[0] and "decode_merge" in launched[1], launched
