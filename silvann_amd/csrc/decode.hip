@@ -65,7 +65,7 @@ struct DecodeArgs {
     uint32_t chunk, nsplit;
     float scale;
     float* part;
-    const uint32_t* plan;   // plan[u]: splits of rows before u; plan[rows]: all splits
+    const uint32_t* plan;   // decode_plan's: full splits of rows before u, all splits, the short splits' rows
     uint32_t* counter;      // the next work item
     uint32_t rows;
     // the fused finish: a count of finished splits a (row, kv head, head block), the answers, the fault word
@@ -79,11 +79,11 @@ struct DecodeArgs {
     uint64_t tag;   // the fused finish with the inline plan: this call's tag for the counts (below kTagMask)
 };
 
-// The scratch: the work counter, the plan, the finished-split counts (rows · kv heads · head blocks, 8 bytes each:
+// The scratch: the work counter, the plan (2·rows + 2 words, below), the finished-split counts (rows · kv heads · head blocks, 8 bytes each:
 // 32-bit counts, or the inline plan's tagged 64-bit words), then the partial residuals
 // [row][q head][split][head_dim + 2].
 constexpr uint64_t kPlanAt = 64;
-uint64_t done_at(uint64_t rows) { return (kPlanAt + 4 * (rows + 1) + 7) / 8 * 8; }
+uint64_t done_at(uint64_t rows) { return (kPlanAt + 4 * (2 * rows + 2) + 7) / 8 * 8; }
 uint64_t part_at(uint64_t rows, uint64_t units) { return (done_at(rows) + 8 * rows * units + 255) / 256 * 256; }
 // A tagged finished-split count: the call's tag in the top 40 bits, the count below. A word holding another tag
 // (an earlier call's, or whatever the scratch held) counts as zero, so no launch has to clear the counts first.
@@ -95,9 +95,17 @@ constexpr uint64_t kMaxGroups = (1ull << 32) / kThreads - 8;
 // The grid of the shared-tile form: its XCD-aware order covers the splits in groups of 8.
 uint32_t shared_grid(uint64_t splits, uint64_t units) { return (uint32_t)((splits + 7) / 8 * 8 * units); }
 
-// Each row's split count, prefix-summed into plan[0..rows], and the counter zeroed. One workgroup. FUSED: also
-// the finished-split counts zeroed, and the answers of rows with no positions written as zeros (no split of
-// theirs will finish them).
+// The plan: each row's full splits (len / chunk) prefix-summed into plan[0..rows] (plan[rows] = F, every row's full
+// splits), the count of all splits at plan[rows + 1], and after it, plan[rows + 2 ..], the rows whose last split is
+// shorter than a chunk, longest remainder first (by 64 buckets of chunk / 64). decode_split takes its items in that
+// order — every full split, then the short ones from the longest — so the last round of work items, the one the
+// chip is not full for, is made of the shortest ones. One workgroup; the counter zeroed. FUSED: also the
+// finished-split counts zeroed, and the answers of rows with no positions written as zeros (no split of theirs
+// will finish them).
+constexpr uint32_t kRemBuckets = 64;
+__device__ __forceinline__ uint32_t rem_bucket(uint32_t rem, uint32_t chunk) {
+    return kRemBuckets - 1 - (uint32_t)((uint64_t)rem * kRemBuckets / chunk);   // bucket 0: the longest remainders
+}
 template <bool FUSED = false>
 __global__ __launch_bounds__(256) void decode_plan(const uint32_t* lens, uint32_t rows, uint32_t chunk, uint32_t* plan,
                                                    uint32_t* counter, uint32_t* done = nullptr, uint32_t units = 0,
@@ -110,14 +118,18 @@ __global__ __launch_bounds__(256) void decode_plan(const uint32_t* lens, uint32_
     }
     __shared__ uint32_t scan[256];
     __shared__ uint32_t carry;
+    __shared__ uint32_t bucket[kRemBuckets];
     if (threadIdx.x == 0) {
         counter[0] = 0;
         carry = 0;
     }
+    if (threadIdx.x < kRemBuckets) bucket[threadIdx.x] = 0;
     __syncthreads();
     for (uint32_t base = 0; base < rows; base += 256) {
         const uint32_t u = base + threadIdx.x;
-        const uint32_t n = u < rows ? (lens[u] + chunk - 1) / chunk : 0;
+        const uint32_t len = u < rows ? lens[u] : 0;
+        const uint32_t n = len / chunk, rem = len % chunk;
+        if (rem) atomicAdd(&bucket[rem_bucket(rem, chunk)], 1u);
         scan[threadIdx.x] = n;
         __syncthreads();
         for (int off = 1; off < 256; off <<= 1) {   // inclusive scan
@@ -131,7 +143,21 @@ __global__ __launch_bounds__(256) void decode_plan(const uint32_t* lens, uint32_
         if (threadIdx.x == 255) carry += scan[255];
         __syncthreads();
     }
-    if (threadIdx.x == 0) plan[rows] = carry;
+    if (threadIdx.x == 0) {   // the buckets' starts, longest first
+        uint32_t at = 0;
+        for (uint32_t b = 0; b < kRemBuckets; ++b) {
+            const uint32_t c = bucket[b];
+            bucket[b] = at;
+            at += c;
+        }
+        plan[rows] = carry;
+        plan[rows + 1] = carry + at;
+    }
+    __syncthreads();
+    for (uint32_t u = threadIdx.x; u < rows; u += 256) {
+        const uint32_t rem = lens[u] % chunk;
+        if (rem) plan[rows + 2 + atomicAdd(&bucket[rem_bucket(rem, chunk)], 1u)] = u;
+    }
 }
 
 // Where the 16 keys from position `t` of row `u`, kv head `g` start in a plane: through the page table (a
@@ -225,7 +251,7 @@ void decode_split(DecodeArgs a) {
             }
         }
     }
-    const uint32_t total = INLINE ? inline_total : a.plan[a.rows] * GH;
+    const uint32_t total = INLINE ? inline_total : a.plan[a.rows + 1] * GH;
     __shared__ uint32_t is_last;
     // the workgroup's item: its own index
     uint32_t item = blockIdx.x;
@@ -238,18 +264,26 @@ void decode_split(DecodeArgs a) {
     }
     if (item >= total) return;
     const uint32_t sidx = item / GH, gh = item % GH;
-    uint32_t lo = 0, hi = a.rows;
+    uint32_t lo = 0, hi = a.rows, s;
     if constexpr (INLINE) {
         // lane 0 (no splits before it) always counts, so lo is a row
         lo = (uint32_t)__builtin_popcountll(__builtin_amdgcn_ballot_w64(lane < (int)a.rows && lane_before <= sidx)) - 1u;
+        s = sidx - (uint32_t)__builtin_amdgcn_readlane((int)lane_before, (int)lo);
     } else {
-        while (hi - lo > 1) {
-            const uint32_t mid = (lo + hi) >> 1;
-            if (a.plan[mid] <= sidx) lo = mid;
-            else hi = mid;
+        const uint32_t full = a.plan[a.rows];
+        if (sidx < full) {   // a full split: the row whose full splits hold index sidx
+            while (hi - lo > 1) {
+                const uint32_t mid = (lo + hi) >> 1;
+                if (a.plan[mid] <= sidx) lo = mid;
+                else hi = mid;
+            }
+            s = sidx - a.plan[lo];
+        } else {             // a row's shorter last split, after every full one
+            lo = a.plan[a.rows + 2 + (sidx - full)];
+            s = a.plan[lo + 1] - a.plan[lo];
         }
     }
-    const uint32_t u = lo, s = sidx - (INLINE ? (uint32_t)__builtin_amdgcn_readlane((int)lane_before, (int)lo) : a.plan[lo]);
+    const uint32_t u = lo;
     const uint32_t g = gh / a.hblocks, hb = gh % a.hblocks;
     const uint32_t len = INLINE ? (uint32_t)__builtin_amdgcn_readlane((int)lane_len, (int)u) : a.lens[u];
     const uint32_t start = s * a.chunk;
@@ -568,13 +602,15 @@ __global__ __launch_bounds__(64 * kMergeWaves) void decode_merge(uint16_t* o, co
     if (hit) *over = kFaultOverflow;
 }
 
-// One row of a uniform length: its length where decode_split reads it, its one-row plan, the counter zeroed — the
-// plan of the deferred door pairs, whose one query's length is a host value.
-__global__ void decode_plan_one(uint32_t* lens, uint32_t length, uint32_t nsplit, uint32_t* plan, uint32_t* counter) {
+// One row of a uniform length: its length where decode_split reads it, its one-row plan (as decode_plan lays it
+// out), the counter zeroed — the plan of the deferred door pairs, whose one query's length is a host value.
+__global__ void decode_plan_one(uint32_t* lens, uint32_t length, uint32_t chunk, uint32_t* plan, uint32_t* counter) {
     if (threadIdx.x == 0) {
         lens[0] = length;
         plan[0] = 0;
-        plan[1] = nsplit;
+        plan[1] = length / chunk;                  // the full splits
+        plan[2] = (length + chunk - 1) / chunk;    // all splits
+        plan[3] = 0;                               // the row of the shorter last split, if there is one
         counter[0] = 0;
     }
 }
@@ -944,7 +980,7 @@ bool decode_one(uint16_t* o, float* res, const uint16_t* q, const uint16_t* k, c
         a.lens_out = lens;
         split_contiguous<true>(a, head_dim, k == v, nsplit, st);
     } else {
-        decode_plan_one<<<1, 64, 0, st>>>(lens, (uint32_t)length, (uint32_t)nsplit, (uint32_t*)a.plan, a.counter);
+        decode_plan_one<<<1, 64, 0, st>>>(lens, (uint32_t)length, a.chunk, (uint32_t*)a.plan, a.counter);
         split_contiguous<false>(a, head_dim, k == v, nsplit, st);
     }
     prof_end(kProfDecodeSplit);

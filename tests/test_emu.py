@@ -52,6 +52,10 @@ def test_causal_pipe_kernel(oracle, hd, qh, kvh, first, rows, ps):
     (16, 2, 256, [700, 2048], 256),        # paged rows of different lengths
     (8, 2, 128, [1, 17, 300], 0),          # contiguous, a one-position row
     (4, 4, 64, [33, 250], 16),             # pages shorter than a tile: one lookup a 16-key group
+    # the plan's order (full splits, then the shorter last ones, longest first) at a 256-position chunk: exact
+    # multiples (no short split), rows shorter than a chunk (only a short one), empty rows
+    (8, 2, 128, [256, 512, 300, 0, 1, 255, 257, 1024, 0, 769], 0),
+    (4, 1, 64, [(i * 37) % 700 for i in range(300)], 32),   # more rows than the plan's 256 threads
 ])
 def test_decode(oracle, qh, kvh, hd, lens, ps):
     w = W.decode("emu", qh, kvh, hd, lens, page_size=ps, seed=hd + len(lens))
