@@ -321,10 +321,14 @@ void decode_split(DecodeArgs a) {
         // the tile's bases: one page-table lookup a tile, or one a 16-key group when pages are shorter
         const uint16_t* kg[NG];
         const uint16_t* vg[NG];
+        // (groups past the split's last key, never read from — their keys take key 0 — alias its last group, so no
+        // page-table entry past the row's is looked up)
+        const uint32_t last_group = (nvalid - 1) / 16;
 #pragma unroll
         for (int p = 0; p < NG; ++p) {
-            kg[p] = group_base(a.k, a, u, g, t0 + 16 * p, row, HD);
-            vg[p] = group_base(a.v, a, u, g, t0 + 16 * p, row, HD);
+            const uint32_t t = t0 + 16 * min((uint32_t)p, last_group);
+            kg[p] = group_base(a.k, a, u, g, t, row, HD);
+            vg[p] = group_base(a.v, a, u, g, t, row, HD);
         }
 
         // K as the A operand: lane (col, grp) reads key 16·p + col, dims 32·ks + 8·grp .. +8. Keys past the

@@ -274,7 +274,7 @@ def test_unaligned_operands_run_door_by_door(oracle, kind, misalign):
         want_p = oracle.scores(q, k, qh, kvh, hd, length)
         want_o, _ = oracle.mix(want_p, v, qh, kvh, hd, length)
     else:
-        qh, kvh, hd, first, rows = 16, 2, 256, 77, 95
+        qh, kvh, hd, first, rows = 8, 2, 64, 10, 40
         q, k, v = _inputs(92, qh, kvh, hd, first + rows, rows)
         o, p, over, _ = emu.run_chain("causal", q, k, v, qh, kvh, hd, first, rows, extra_env=env)
         want_o, _ = oracle.causal_rows(q, k, v, None, 0, qh, kvh, hd, first, list(range(rows)))
