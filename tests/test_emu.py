@@ -140,7 +140,7 @@ INLINE = {"SILVANN_GFX950_DECODE_INLINE": "1", "EMU_LAUNCHES": "1"}
 @pytest.mark.parametrize("qh,kvh,hd,lens,ps", [
     (16, 2, 256, [700, 0, 2048, 0], 256),                  # empty rows between and last
     (8, 2, 128, [0, 1, 17, 3000, 5], 0),                   # an empty first row; many splits beside one-split rows
-    (4, 4, 64, [(37 * i) % 150 for i in range(64)], 16),   # 64 rows (the inline plan's most), pages shorter than a tile
+    (4, 1, 64, [(37 * i) % 150 for i in range(64)], 16),   # 64 rows (the inline plan's most), pages shorter than a tile
 ])
 def test_decode_inline_plan(oracle, qh, kvh, hd, lens, ps):
     """Row 137 with its plan made inside decode_split (SILVANN_GFX950_DECODE_INLINE=1: each wave's prefix scan of
@@ -158,7 +158,7 @@ def test_decode_inline_plan(oracle, qh, kvh, hd, lens, ps):
 @pytest.mark.parametrize("qh,kvh,hd,lens,ps", [
     (16, 2, 256, [700, 0, 2048, 0], 256),                  # empty rows: zero answers from workgroup 0
     (8, 2, 128, [1, 17, 3000], 0),                         # a row of many splits beside one-split rows
-    (4, 4, 64, [(37 * i) % 150 for i in range(64)], 16),   # 64 rows, pages shorter than a tile
+    (4, 1, 64, [(37 * i) % 150 for i in range(64)], 16),   # 64 rows, pages shorter than a tile
 ])
 @pytest.mark.parametrize("repeat", [False, True])
 def test_decode_one_launch(oracle, qh, kvh, hd, lens, ps, repeat):
