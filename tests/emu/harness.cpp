@@ -14,6 +14,31 @@
 #include "emu_rt.hpp"
 #include "silvann_gfx950_attention.h"
 
+// The lanes' context switch (emu_rt.hpp): push the callee-saved registers, keep the stack pointer in *save_sp (rdi),
+// take load_sp (rsi) as the stack pointer, pop that context's callee-saved registers and return into it.
+asm(R"(
+    .text
+    .globl emu_ctx_switch
+    .type emu_ctx_switch, @function
+emu_ctx_switch:
+    pushq %rbp
+    pushq %rbx
+    pushq %r12
+    pushq %r13
+    pushq %r14
+    pushq %r15
+    movq %rsp, (%rdi)
+    movq %rsi, %rsp
+    popq %r15
+    popq %r14
+    popq %r13
+    popq %r12
+    popq %rbx
+    popq %rbp
+    ret
+    .size emu_ctx_switch, .-emu_ctx_switch
+)");
+
 namespace silvann {
 extern int emu_refused;
 void flush_deferred();
