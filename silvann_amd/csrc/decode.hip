@@ -70,6 +70,8 @@ struct DecodeArgs {
     uint32_t rows;
     // the fused finish: a count of finished splits a (row, kv head, head block), the answers, the fault word
     uint32_t* done;
+    uint32_t* gdone = nullptr;   // rows of more than kFinishGroup splits: a count a group of them, maxng a unit
+    uint32_t maxng = 0;
     uint16_t* o;
     unsigned int* over;
     // the inline plan with lens null: row u's length is len_first + u·len_step, and workgroup 0 writes the lengths
@@ -84,7 +86,13 @@ struct DecodeArgs {
 // [row][q head][split][head_dim + 2].
 constexpr uint64_t kPlanAt = 64;
 uint64_t done_at(uint64_t rows) { return (kPlanAt + 4 * (2 * rows + 2) + 7) / 8 * 8; }
-uint64_t part_at(uint64_t rows, uint64_t units) { return (done_at(rows) + 8 * rows * units + 255) / 256 * 256; }
+// The fused finish's groups: a row of more than kFinishGroup splits finishes in two levels (decode_split).
+constexpr uint32_t kFinishGroup = 32;
+uint64_t groups_at(uint64_t rows, uint64_t units) { return done_at(rows) + 8 * rows * units; }
+// `maxng` count words a (row, kv head, head block) after the finished-split counts: the groups' (row 137's scratch)
+uint64_t part_at(uint64_t rows, uint64_t units, uint64_t maxng = 0) {
+    return (groups_at(rows, units) + 8 * rows * units * maxng + 255) / 256 * 256;
+}
 // A tagged finished-split count: the call's tag in the top 40 bits, the count below. A word holding another tag
 // (an earlier call's, or whatever the scratch held) counts as zero, so no launch has to clear the counts first.
 constexpr int kTagShift = 24;
@@ -109,9 +117,11 @@ __device__ __forceinline__ uint32_t rem_bucket(uint32_t rem, uint32_t chunk) {
 template <bool FUSED = false>
 __global__ __launch_bounds__(256) void decode_plan(const uint32_t* lens, uint32_t rows, uint32_t chunk, uint32_t* plan,
                                                    uint32_t* counter, uint32_t* done = nullptr, uint32_t units = 0,
-                                                   uint16_t* o = nullptr, uint32_t row_halves = 0) {
+                                                   uint16_t* o = nullptr, uint32_t row_halves = 0,
+                                                   uint32_t* gdone = nullptr, uint32_t maxng = 0) {
     if constexpr (FUSED) {
         for (uint32_t i = threadIdx.x; i < rows * units; i += 256) done[i] = 0;
+        for (uint32_t i = threadIdx.x; i < rows * units * maxng; i += 256) gdone[i] = 0;
         for (uint32_t u = 0; u < rows; ++u)
             if (lens[u] == 0)
                 for (uint32_t i = threadIdx.x; i < row_halves; i += 256) o[(uint64_t)u * row_halves + i] = 0;
@@ -470,15 +480,23 @@ void decode_split(DecodeArgs a) {
         }
     }
     if constexpr (FUSED) {
-        // Release this split's residual device-wide, then count it in; the split that makes the count whole
-        // acquires the others' and finishes the heads.
+        // Release this split's residual device-wide, then count it in. A row of at most kFinishGroup splits: the
+        // split that makes the row's count whole acquires the others' residuals and finishes the heads. A longer
+        // row finishes in two levels, so no one workgroup reads every split's residual: the split that completes
+        // its group of kFinishGroup merges the group, exactly, into the group's first slot, then counts the group
+        // in, and the group that completes the row finishes the heads from the group slots.
         __threadfence();
         __syncthreads();
         const uint32_t ns = (len + a.chunk - 1) / a.chunk;
-        if (threadIdx.x == 0) {
+        const uint32_t ng = (ns + kFinishGroup - 1) / kFinishGroup;
+        const uint32_t gi = s / kFinishGroup, g0 = gi * kFinishGroup, gsz = min(kFinishGroup, ns - g0);
+        const uint64_t unit = (uint64_t)u * GH + gh;
+        const float* base = a.part + ((uint64_t)u * a.q_heads + h0) * a.nsplit * (HD + 2);
+        // count one in at entry i of a plane of counts; answers whether that made `total`
+        auto count_in = [&](uint32_t* plane, uint64_t i, uint32_t total) -> bool {
             if constexpr (INLINE) {
                 // no plan launch cleared the count: a word of another tag is a count of zero
-                unsigned long long* word = (unsigned long long*)a.done + (uint64_t)u * GH + gh;
+                unsigned long long* word = (unsigned long long*)plane + i;
                 unsigned long long seen = *(volatile unsigned long long*)word, was;   // a guess the CAS corrects
                 uint32_t count;
                 do {
@@ -486,23 +504,22 @@ void decode_split(DecodeArgs a) {
                     count = (was >> kTagShift) == a.tag ? (uint32_t)(was & ((1u << kTagShift) - 1)) : 0u;
                     seen = atomicCAS(word, was, (a.tag << kTagShift) | (count + 1u));
                 } while (seen != was);
-                is_last = count == ns - 1;
+                return count == total - 1;
             } else {
-                is_last = atomicAdd(a.done + (uint64_t)u * GH + gh, 1u) == ns - 1;
+                return atomicAdd(plane + i, 1u) == total - 1;
             }
-        }
-        __syncthreads();
-        if (is_last) {
-            __threadfence();
-            const float* base = a.part + ((uint64_t)u * a.q_heads + h0) * a.nsplit * (HD + 2);
-            // a wave a head at a time: the largest m over the splits, then l = Σ e^(m_s - M)·l_s
+        };
+        // the answers from `count` residuals, slot q at q·stride: a wave a head for the largest m and
+        // l = Σ e^(m_s - M)·l_s, then a lane a (head, dim) for acc / l
+        auto finish = [&](uint32_t count, uint32_t stride) {
             for (int hh = w; hh < nh; hh += kWaves) {
                 const float* ph = base + (uint64_t)hh * a.nsplit * (HD + 2);
                 float mm = -INFINITY;
-                for (uint32_t q = lane; q < ns; q += 64) mm = fmaxf(mm, ph[(uint64_t)q * (HD + 2)]);
+                for (uint32_t q = lane; q < count; q += 64) mm = fmaxf(mm, ph[(uint64_t)q * stride * (HD + 2)]);
                 mm = wave_max(mm);
                 float ll = 0.0f;
-                for (uint32_t q = lane; q < ns; q += 64) ll += fast_exp(ph[(uint64_t)q * (HD + 2)] - mm) * ph[(uint64_t)q * (HD + 2) + 1];
+                for (uint32_t q = lane; q < count; q += 64)
+                    ll += fast_exp(ph[(uint64_t)q * stride * (HD + 2)] - mm) * ph[(uint64_t)q * stride * (HD + 2) + 1];
                 ll = wave_sum(ll);
                 if (lane == 0) {
                     ms[hh] = mm;
@@ -516,10 +533,59 @@ void decode_split(DecodeArgs a) {
                 const float* ph = base + (uint64_t)hh * a.nsplit * (HD + 2);
                 const float mm = ms[hh];
                 float acc = 0.0f;
-                for (uint32_t q = 0; q < ns; ++q) acc += fast_exp(ph[(uint64_t)q * (HD + 2)] - mm) * ph[(uint64_t)q * (HD + 2) + 2 + d];
+                for (uint32_t q = 0; q < count; ++q)
+                    acc += fast_exp(ph[(uint64_t)q * stride * (HD + 2)] - mm) * ph[(uint64_t)q * stride * (HD + 2) + 2 + d];
                 a.o[((uint64_t)u * a.q_heads + h0 + hh) * HD + d] = to_half(acc / ls[hh], hit);
             }
             if (hit) *a.over = kFaultOverflow;
+        };
+        if (threadIdx.x == 0)
+            is_last = ng == 1 ? count_in(a.done, unit, ns) : count_in(a.gdone, unit * a.maxng + gi, gsz);
+        __syncthreads();
+        if (is_last) {
+            __threadfence();
+            if (ng == 1) {
+                finish(ns, 1);
+            } else {
+                // the group's residual into slot g0: each split's weight e^(m_s - M) a head (a lane a split), then
+                // a lane a (head, dim) sums its column in place, then the head's M and l
+                __shared__ float gw[16 * kFinishGroup];
+                for (int hh = w; hh < nh; hh += kWaves) {
+                    const float* ph = base + (uint64_t)hh * a.nsplit * (HD + 2) + (uint64_t)g0 * (HD + 2);
+                    const float m_s = lane < (int)gsz ? ph[(uint64_t)lane * (HD + 2)] : -INFINITY;
+                    const float mm = wave_max(m_s);
+                    const float wt = lane < (int)gsz ? fast_exp(m_s - mm) : 0.0f;
+                    const float ll = wave_sum(lane < (int)gsz ? wt * ph[(uint64_t)lane * (HD + 2) + 1] : 0.0f);
+                    if (lane < (int)gsz) gw[hh * kFinishGroup + lane] = wt;
+                    if (lane == 0) {
+                        ms[hh] = mm;
+                        ls[hh] = ll;
+                    }
+                }
+                __syncthreads();
+                for (int idx = threadIdx.x; idx < nh * HD; idx += kThreads) {
+                    const int hh = idx / HD, d = idx % HD;
+                    float* ph = (float*)base + (uint64_t)hh * a.nsplit * (HD + 2) + (uint64_t)g0 * (HD + 2);
+                    float acc = 0.0f;
+                    for (uint32_t j = 0; j < gsz; ++j) acc += gw[hh * kFinishGroup + j] * ph[(uint64_t)j * (HD + 2) + 2 + d];
+                    ph[2 + d] = acc;
+                }
+                __syncthreads();
+                if ((int)threadIdx.x < nh) {
+                    float* ph = (float*)base + (uint64_t)threadIdx.x * a.nsplit * (HD + 2) + (uint64_t)g0 * (HD + 2);
+                    ph[0] = ms[threadIdx.x];
+                    ph[1] = ls[threadIdx.x];
+                }
+                // release the group's residual, then count the group in; the group that completes the row finishes
+                __threadfence();
+                __syncthreads();
+                if (threadIdx.x == 0) is_last = count_in(a.done, unit, ng);
+                __syncthreads();
+                if (is_last) {
+                    __threadfence();
+                    finish(ng, kFinishGroup);
+                }
+            }
         }
     }
 }
@@ -708,11 +774,7 @@ bool vtr() {
     return on;
 }
 
-// The fused finish (SILVANN_GFX950_DECODE_FUSED=1): checked in the CPU emulation, not yet measured on a GPU. It is
-// taken only for rows of at most kFusedMaxSplits splits: its one finishing workgroup a (row, kv head, head block)
-// reads every split's residual alone — at C5's 256 splits of 8 heads × 258 floats, 2.1 MB through one CU — where
-// decode_merge spreads that over a workgroup a (head, 64 dims).
-constexpr uint32_t kFusedMaxSplits = 32;
+// The fused finish (SILVANN_GFX950_DECODE_FUSED=1): checked in the CPU emulation, not yet measured on a GPU.
 bool fused_finish() {
     static const bool on = [] {
         const char* e = getenv("SILVANN_GFX950_DECODE_FUSED");
@@ -797,7 +859,9 @@ void decode_paged_launch(uint16_t* o, const uint16_t* q, const uint16_t* k, cons
     a.counter = (uint32_t*)scratch;
     a.plan = (const uint32_t*)((char*)scratch + kPlanAt);
     a.done = (uint32_t*)((char*)scratch + done_at(rows));
-    a.part = (float*)((char*)scratch + part_at(rows, kv_heads * a.hblocks));
+    a.maxng = (a.nsplit + kFinishGroup - 1) / kFinishGroup;
+    a.gdone = (uint32_t*)((char*)scratch + groups_at(rows, kv_heads * a.hblocks));
+    a.part = (float*)((char*)scratch + part_at(rows, kv_heads * a.hblocks, a.maxng));
     a.rows = (uint32_t)rows;
     a.o = o;
     a.over = over;
@@ -819,7 +883,7 @@ void decode_paged_launch(uint16_t* o, const uint16_t* q, const uint16_t* k, cons
         return;
     }
     const dim3 igrid((uint32_t)items);
-    const bool fused = fused_finish() && a.nsplit <= kFusedMaxSplits;
+    const bool fused = fused_finish();
     if (fused && head_dim <= 256 && inline_plan() && rows <= 64) {
         // one launch: the plan made in the kernel, the counts tagged with this call's tag
         a.tag = next_tag();
@@ -841,7 +905,7 @@ void decode_paged_launch(uint16_t* o, const uint16_t* q, const uint16_t* k, cons
     if (fused && head_dim <= 256) {
         const uint32_t units = a.kv_heads * a.hblocks;
         decode_plan<true><<<1, 256, 0, st>>>(lens, a.rows, a.chunk, (uint32_t*)a.plan, a.counter, a.done, units, o,
-                                             a.q_heads * (uint32_t)head_dim);
+                                             a.q_heads * (uint32_t)head_dim, a.gdone, a.maxng);
         prof_begin(kProfDecodeSplit);
         const uint32_t hv = (uint32_t)head_dim;
         if (grouped) {
@@ -965,7 +1029,7 @@ bool decode_one(uint16_t* o, float* res, const uint16_t* q, const uint16_t* k, c
     a.tag = 0;
     hipStream_t st = stream();
     prof_begin(kProfDecodeSplit);
-    if (o && !sink && head_dim <= 256 && inline_plan() && fused_finish() && nsplit <= kFusedMaxSplits) {
+    if (o && !sink && head_dim <= 256 && inline_plan() && fused_finish() && nsplit <= kFinishGroup) {
         // one launch: the last split of each head block finishes the answers, its counts tagged
         a.lens = nullptr;
         a.len_first = (uint32_t)length;
@@ -1150,7 +1214,9 @@ uint64_t decode_paged_scratch(uint64_t q_heads, uint64_t kv_heads, uint64_t head
     if (!decode_shape_ok(q_heads, kv_heads, head_dim, most, rows)) return 0;
     const uint32_t chunk = choose_chunk(head_dim, kv_heads, head_blocks(q_heads, kv_heads), most, rows);
     const uint64_t nsplit = (most + chunk - 1) / chunk;
-    return part_at(rows, kv_heads * head_blocks(q_heads, kv_heads)) + rows * q_heads * nsplit * (head_dim + 2) * sizeof(float);
+    const uint64_t maxng = (nsplit + kFinishGroup - 1) / kFinishGroup;
+    return part_at(rows, kv_heads * head_blocks(q_heads, kv_heads), maxng) +
+           rows * q_heads * nsplit * (head_dim + 2) * sizeof(float);
 }
 
 }  // namespace silvann

@@ -177,14 +177,20 @@ def test_decode_one_launch(oracle, qh, kvh, hd, lens, ps, repeat):
     assert len(launched) == 1 + repeat and all("decode_split" in x for x in launched), launched
 
 
-def test_decode_long_rows_keep_the_merge_launch(oracle):
-    """With the fused finish and the inline plan switched on, a row of more than 32 splits (here 40) keeps the
-    merge launch: one finishing workgroup would read every split's residual alone. The answers are the oracle's."""
-    w = W.decode("emu", 4, 4, 64, [20000, 300], page_size=0, seed=77)
-    got, over, log = emu.run_decode(w, env={**FUSED, **INLINE})
+@pytest.mark.parametrize("inline,repeat", [(False, False), (True, False), (True, True)])
+def test_decode_fused_finish_in_two_levels(oracle, inline, repeat):
+    """Rows of more than 32 splits (40 and 34 here, beside a one-split row) with the fused finish: each group of 32
+    splits is merged by its last split into the group's first slot, and the group that completes the row finishes
+    it, so no workgroup reads every split's residual. No merge launch; with the inline plan, one launch — also over
+    the counts a first call left (`repeat`). The answers are the oracle's."""
+    w = W.decode("emu", 4, 4, 64, [20000, 300, 17000], page_size=0, seed=77)
+    env = {**FUSED, **(INLINE if inline else {"EMU_LAUNCHES": "1"}), **({"EMU_REPEAT": "1"} if repeat else {})}
+    got, over, log = emu.run_decode(w, env=env)
     want, _ = oracle.decode_paged(w.q, w.k, w.v, w.pages, w.pages_row, w.page_size, w.k_row, w.lens, 4, 4, 64,
                                   w.rows)
     parity(got, want)
     assert over == 0
     launched = [ln for ln in log.splitlines() if ln.startswith("emu launch ")]
-    assert len(launched) == 2 and "decode_split" in launched[0] and "decode_merge" in launched[1], launched
+    splits = [x for x in launched if "decode_split" in x]
+    assert not any("decode_merge" in x for x in launched), launched
+    assert len(splits) == 1 + repeat and len(launched) == (1 + repeat) * (1 if inline else 2), launched
