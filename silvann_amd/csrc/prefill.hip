@@ -41,6 +41,9 @@ namespace {
 #ifndef SILVANN_PREFILL_VA
 #define SILVANN_PREFILL_VA 2
 #endif
+#ifndef SILVANN_PREFILL_UNIFORM_WAVE
+#define SILVANN_PREFILL_UNIFORM_WAVE 0
+#endif
 #ifndef SILVANN_PREFILL_XCD_ORDER   // 0: workgroups in launch order (an experiment build's comparison)
 #define SILVANN_PREFILL_XCD_ORDER 1
 #endif
@@ -147,7 +150,10 @@ __global__ __launch_bounds__(kThreads) void causal_mfma(CausalArgs a) {
     __shared__ __attribute__((aligned(16))) Stage<HD> ring[kStages];
     __shared__ uint32_t pt[PTL ? kPagesInLds : 1];   // the sequence's page table, off the memory counter
 
-    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    // SILVANN_PREFILL_UNIFORM_WAVE=1 (an experiment build): the wave index through readfirstlane, so every
+    // loop bound and branch derived from it is lowered as wave-uniform, the generic tile loop's too
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int w = SILVANN_PREFILL_UNIFORM_WAVE ? __builtin_amdgcn_readfirstlane(tid >> 6) : tid >> 6;
     const int col = lane & 31, half = lane >> 5;
     const Block blk = xcd_block();
     const uint32_t g = blk.y / a.hblocks, hb = blk.y % a.hblocks;
