@@ -479,6 +479,8 @@ def main():
             secondary.append(isolated(2, a.steps, a.warmup,
                                       env={"SILVANN_GFX950_DECODE_INLINE": "1", "SILVANN_GFX950_DECODE_FUSED": "1"},
                                       variant="one launch a step (inline plan + fused finish)"))
+            secondary.append(isolated(9, max(5, a.steps // 2), a.warmup, env={"SILVANN_GFX950_DECODE_LATENT": "wide"},
+                                      variant="latent attention, four head blocks a workgroup (decode_latent)"))
             for n in (1, 5):   # the launch-bound and the longest decode in one launch
                 secondary.append(isolated(n, max(5, a.steps // 2), a.warmup,
                                           env={"SILVANN_GFX950_DECODE_INLINE": "1", "SILVANN_GFX950_DECODE_FUSED": "1"},

@@ -41,6 +41,7 @@
 #include <random>
 #include <stdio.h>
 #include <stdlib.h>
+#include <string.h>
 
 #include "common.hpp"
 #include "../../include/silvann_gfx950_attention.h"
@@ -590,6 +591,178 @@ void decode_split(DecodeArgs a) {
     }
 }
 
+// head_dim 512 with the keys the values (latent attention), opt-in (SILVANN_GFX950_DECODE_LATENT=wide): one
+// workgroup a (split, kv head, four head blocks), its four waves each a head block of up to 16 query heads, so each
+// latent tile comes from L2 into LDS once for up to 64 heads — where decode_split<512, …, SHARED> brings it once for
+// each head block's workgroup. The tiles (32 latents, 32 KB) go HBM → LDS directly through a ring of four stages,
+// every wave loading an eighth of each: tile t + 3 is in flight while tile t computes, one barrier a tile. A wave
+// past the group's head blocks loads and meets the barriers but computes nothing. No merge across the waves: each
+// writes its head block's residual, which decode_merge joins as decode_split's.
+constexpr int kLatentBlocks = 4;   // head blocks a workgroup
+constexpr int kLatentStages = 4;
+constexpr int vmcnt_only(int n) { return 0x0F70 | (n & 0xF) | ((n >> 4) << 14); }
+template <bool GROUPED>
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1)))
+void decode_latent(DecodeArgs a) {
+    constexpr int HD = 512, TK = 32, MT = TK / 16, KS = HD / 32, NT = HD / 16, CPR = HD / 8;
+    constexpr int kStage = TK * HD;                 // halves a stage
+    constexpr int LOADS = TK * CPR / kThreads;      // 16-byte loads a thread a tile
+    __shared__ __attribute__((aligned(16))) _Float16 ring[kLatentStages * kStage];
+
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    const int col = lane & 15, grp = lane >> 4;
+    const uint64_t row = (uint64_t)a.kv_heads * HD;
+    const uint32_t units = (a.hblocks + kLatentBlocks - 1) / kLatentBlocks, GH = a.kv_heads * units;
+    const uint32_t item = blockIdx.x;
+    if (item >= a.plan[a.rows + 1] * GH) return;
+    const uint32_t sidx = item / GH, gh = item % GH;
+    uint32_t u, s;
+    {
+        const uint32_t full = a.plan[a.rows];
+        if (sidx < full) {
+            uint32_t lo = 0, hi = a.rows;
+            while (hi - lo > 1) {
+                const uint32_t mid = (lo + hi) >> 1;
+                if (a.plan[mid] <= sidx) lo = mid;
+                else hi = mid;
+            }
+            u = lo;
+            s = sidx - a.plan[lo];
+        } else {
+            u = a.plan[a.rows + 2 + (sidx - full)];
+            s = a.plan[u + 1] - a.plan[u];
+        }
+    }
+    const uint32_t g = gh / units, hb = (gh % units) * kLatentBlocks + w;
+    const bool active = hb < a.hblocks;
+    const uint32_t len = a.lens[u], start = s * a.chunk, end = min(len, start + a.chunk);
+    const uint32_t h0 = g * a.group + hb * 16;
+    const int nh = active ? min(16, (int)(a.group - hb * 16)) : 0;
+
+    f16x8 qb[KS];
+    {
+        const uint16_t* qh = a.q + ((uint64_t)u * a.q_heads + (active ? h0 : 0) + (col < nh ? col : 0)) * HD;
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) {
+            f16x8 x = *(const f16x8*)(qh + 32 * ks + 8 * grp);
+            qb[ks] = col < nh ? x : (f16x8)0;
+        }
+    }
+    float m = -INFINITY, l = 0.0f;
+    f32x4 acc[NT];
+#pragma unroll
+    for (int n = 0; n < NT; ++n) acc[n] = (f32x4)0.0f;
+
+    const uint32_t ntiles = (end - start + TK - 1) / TK;
+    // tile t into its stage: this wave's slots w·LOADS·64 .. , slot (key, physical chunk) holding the key's logical
+    // chunk chunk ^ f(key); latents past the split bring the tile's latent 0 (masked)
+    auto load_tile = [&](uint32_t t) __attribute__((always_inline)) {
+        const uint32_t t0 = start + t * TK, nvalid = min((uint32_t)TK, end - t0);
+        const uint16_t* gb[GROUPED ? 2 : 1];
+#pragma unroll
+        for (int p = 0; p < (GROUPED ? 2 : 1); ++p)
+            gb[p] = group_base(a.k, a, u, g, t0 + 16 * min((uint32_t)p, (nvalid - 1) / 16), row, HD);
+        _Float16* st = ring + (t % kLatentStages) * kStage;
+#pragma unroll
+        for (int i = 0; i < LOADS; ++i) {
+            const int slot = (w * LOADS + i) * 64 + lane, key = slot / CPR, c = vslot(key, slot % CPR);
+            const int kk = key < (int)nvalid ? key : 0;
+            const uint16_t* src = (GROUPED ? gb[kk >> 4] + (uint64_t)(kk & 15) * row : gb[0] + (uint64_t)kk * row) + 8 * c;
+            dma16_nt(src, (__attribute__((address_space(3))) void*)(st + (w * LOADS + i) * 64 * 8));
+        }
+    };
+    // vector-memory count <= (tiles issued after tile t + 1)·LOADS: tile t + 1 landed
+    auto wait_next = [&](uint32_t t) __attribute__((always_inline)) {
+        const uint32_t after = ntiles > t + 2 ? min(ntiles - t - 2, 2u) : 0u;
+        if (after == 2) __builtin_amdgcn_s_waitcnt(vmcnt_only(2 * LOADS));
+        else if (after == 1) __builtin_amdgcn_s_waitcnt(vmcnt_only(LOADS));
+        else __builtin_amdgcn_s_waitcnt(vmcnt_only(0));
+    };
+
+    load_tile(0);
+    if (ntiles > 1) load_tile(1);
+    if (ntiles > 2) load_tile(2);
+    if (ntiles > 2) __builtin_amdgcn_s_waitcnt(vmcnt_only(2 * LOADS));
+    else if (ntiles > 1) __builtin_amdgcn_s_waitcnt(vmcnt_only(LOADS));
+    else __builtin_amdgcn_s_waitcnt(vmcnt_only(0));
+    __syncthreads();
+    for (uint32_t t = 0; t < ntiles; ++t) {
+        // stage (t + 3) % 4 held tile t - 1, which every wave finished before the last barrier
+        if (t + 3 < ntiles) load_tile(t + 3);
+        if (active) {
+            const _Float16* vs = ring + (t % kLatentStages) * kStage;
+            const uint32_t nvalid = min((uint32_t)TK, end - (start + t * TK));
+            // S^T: lane holds latents 16·p + 4·grp + r of head col
+            float sv[MT * 4];
+#pragma unroll
+            for (int p = 0; p < MT; ++p) {
+                const int key = 16 * p + col;
+                f32x4 st4 = (f32x4)0.0f;
+#pragma unroll
+                for (int ks = 0; ks < KS; ++ks)
+                    st4 = __builtin_amdgcn_mfma_f32_16x16x32_f16(*(const f16x8*)(vs + (key * CPR + vslot(key, 4 * ks + grp)) * 8),
+                                                                qb[ks], st4, 0, 0, 0);
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const int k2 = 16 * p + 4 * grp + r;
+                    sv[4 * p + r] = k2 < (int)nvalid ? st4[r] * a.scale : -INFINITY;
+                }
+            }
+            float mx = sv[0];
+#pragma unroll
+            for (int r = 1; r < MT * 4; ++r) mx = fmaxf(mx, sv[r]);
+            mx = groups_max(mx);
+            const float mnew = fmaxf(m, mx);
+            const float corr = fast_exp(m - mnew);
+            float lsum = 0.0f;
+            f16x8 pb[MT / 2];
+#pragma unroll
+            for (int r = 0; r < MT * 4; ++r) {
+                const float pr = fast_exp(sv[r] - mnew);
+                lsum += pr;
+                pb[r / 8][r % 8] = (_Float16)pr;
+            }
+            l = l * corr + lsum;
+            m = mnew;
+#pragma unroll
+            for (int n = 0; n < NT; ++n) acc[n] *= corr;
+            // O^T += V^T · P^T, V^T through the transposing read: lane 4·jj + rr of block grp points at latent
+            // 32·sp + 4·grp + jj (+ 16), dims 16·n + 4·rr .. +3
+#pragma unroll
+            for (int sp = 0; sp < MT / 2; ++sp)
+#pragma unroll
+                for (int n = 0; n < NT; ++n) {
+                    const int li = lane & 15, jj = li >> 2, d0 = 16 * n + 4 * (li & 3);
+                    const int k0 = 32 * sp + 4 * grp + jj, k1 = k0 + 16;
+                    typedef short s16x4 __attribute__((ext_vector_type(4)));
+                    const s16x4 x0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                        (__attribute__((address_space(3))) s16x4*)(vs + (k0 * CPR + vslot(k0, d0 >> 3)) * 8 + (d0 & 7)));
+                    const s16x4 x1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                        (__attribute__((address_space(3))) s16x4*)(vs + (k1 * CPR + vslot(k1, d0 >> 3)) * 8 + (d0 & 7)));
+                    const f16x8 va = __builtin_bit_cast(f16x8, __builtin_shufflevector(x0, x1, 0, 1, 2, 3, 4, 5, 6, 7));
+                    acc[n] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va, pb[sp], acc[n], 0, 0, 0);
+                }
+        }
+        if (t + 1 < ntiles) {
+            wait_next(t);
+            __syncthreads();   // tile t + 1 is in LDS for every wave; every wave is done reading tile t
+        }
+    }
+    if (!active) return;
+    l = groups_sum(l);
+    if (col < nh) {
+        float* pr = a.part + (((uint64_t)u * a.q_heads + h0 + col) * a.nsplit + s) * (HD + 2);
+#pragma unroll
+        for (int n = 0; n < NT; ++n)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) pr[2 + 16 * n + 4 * grp + r] = acc[n][r];
+        if (grp == 0) {
+            pr[0] = m;
+            pr[1] = l;
+        }
+    }
+}
+
 // Pass 2: a workgroup of 4 or 16 waves (by the split count) per (row, query head, 64 dims). Wave w takes
 // splits w, w + waves, …, eight
 // at a time with eight independent sums (their loads in flight together); a lane holds one dim; the waves'
@@ -803,6 +976,16 @@ bool inline_plan() {
     return on;
 }
 
+// Latent attention's wide form (SILVANN_GFX950_DECODE_LATENT=wide): checked in the CPU emulation, not yet
+// measured on a GPU.
+bool latent_wide() {
+    static const bool on = [] {
+        const char* e = getenv("SILVANN_GFX950_DECODE_LATENT");
+        return e && strcmp(e, "wide") == 0;
+    }();
+    return on;
+}
+
 // decode_split over contiguous caches, one workgroup an item, `splits` = rows · splits a row: head_dim 64-512, the
 // keys-are-values form at 512 when `shared`; INL makes the plan inside the kernel.
 template <bool INL>
@@ -853,7 +1036,10 @@ void decode_paged_launch(uint16_t* o, const uint16_t* q, const uint16_t* k, cons
     a.lens = lens;
     a.q_heads = (uint32_t)q_heads; a.kv_heads = (uint32_t)kv_heads; a.group = (uint32_t)(q_heads / kv_heads);
     a.hblocks = head_blocks(q_heads, kv_heads);
-    a.chunk = choose_chunk(head_dim, kv_heads, a.hblocks, most, rows);
+    // latent attention's wide form: a workgroup takes four head blocks, so a quarter of the units share the chip
+    const bool latent = head_dim == 512 && k == v && latent_wide();
+    const uint32_t lunits = (a.hblocks + kLatentBlocks - 1) / kLatentBlocks;
+    a.chunk = choose_chunk(head_dim, kv_heads, latent ? lunits : a.hblocks, most, rows);
     a.nsplit = (uint32_t)((most + a.chunk - 1) / a.chunk);
     a.scale = 1.0f / sqrtf((float)head_dim);
     a.counter = (uint32_t*)scratch;
@@ -928,7 +1114,11 @@ void decode_paged_launch(uint16_t* o, const uint16_t* q, const uint16_t* k, cons
     // head_dim 512: one workgroup an item; the shared-tile form when the keys are the values
     const bool shared = k == v;
     if (head_dim == 512) {
-        if (shared) {
+        if (shared && latent) {
+            const dim3 lgrid((uint32_t)(rows * a.nsplit * kv_heads * lunits));
+            if (grouped) decode_latent<true><<<lgrid, kThreads, 0, st>>>(a);
+            else decode_latent<false><<<lgrid, kThreads, 0, st>>>(a);
+        } else if (shared) {
             const dim3 sgrid(shared_grid(rows * a.nsplit, kv_heads * a.hblocks));
             if (grouped) decode_split<512, 2, true, true><<<sgrid, kThreads, 0, st>>>(a);
             else decode_split<512, 2, false, true><<<sgrid, kThreads, 0, st>>>(a);
@@ -1212,11 +1402,19 @@ bool decode_rows_fit(uint16_t* o, const uint16_t* q, const uint16_t* k, const ui
 
 uint64_t decode_paged_scratch(uint64_t q_heads, uint64_t kv_heads, uint64_t head_dim, uint64_t most, uint64_t rows) {
     if (!decode_shape_ok(q_heads, kv_heads, head_dim, most, rows)) return 0;
-    const uint32_t chunk = choose_chunk(head_dim, kv_heads, head_blocks(q_heads, kv_heads), most, rows);
-    const uint64_t nsplit = (most + chunk - 1) / chunk;
-    const uint64_t maxng = (nsplit + kFinishGroup - 1) / kFinishGroup;
-    return part_at(rows, kv_heads * head_blocks(q_heads, kv_heads), maxng) +
-           rows * q_heads * nsplit * (head_dim + 2) * sizeof(float);
+    const uint32_t hb = head_blocks(q_heads, kv_heads);
+    auto need = [&](uint64_t units) {   // the chunk a grid of `units` workgroups a split takes
+        const uint32_t chunk = choose_chunk(head_dim, kv_heads, units, most, rows);
+        const uint64_t nsplit = (most + chunk - 1) / chunk;
+        const uint64_t maxng = (nsplit + kFinishGroup - 1) / kFinishGroup;
+        return part_at(rows, kv_heads * hb, maxng) + rows * q_heads * nsplit * (head_dim + 2) * sizeof(float);
+    };
+    // head_dim 512: enough for latent attention's wide form too (its splits are shorter), which the caller may take
+    // (keys the values) or not
+    const uint64_t n = need(hb);
+    if (head_dim != 512) return n;
+    const uint64_t nw = need((hb + kLatentBlocks - 1) / kLatentBlocks);
+    return n > nw ? n : nw;
 }
 
 }  // namespace silvann

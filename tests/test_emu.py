@@ -99,6 +99,25 @@ def test_decode_head_dim_512(oracle, qh, lens, ps, shared):
     assert over == 0
 
 
+@pytest.mark.parametrize("qh,kvh,lens,ps", [
+    (64, 1, [130, 41], 0),             # latent attention's shape: one workgroup a split for all four head blocks
+    (80, 1, [300, 7, 0], 64),          # five head blocks: a second workgroup with one working wave; paged; an empty row
+    (20, 2, [97, 1200], 16),           # two kv heads of 10 heads; pages shorter than a tile; several splits a row
+    (16, 1, [5000], 0),                # one head block (three waves idle), a ring of many tiles
+])
+def test_decode_latent_wide(oracle, qh, kvh, lens, ps):
+    """Row 137 at head_dim 512 with the keys the values in its wide form (SILVANN_GFX950_DECODE_LATENT=wide): a
+    workgroup's four waves take four head blocks of one split over a shared ring of latent tiles. The oracle's decode
+    over the same cache."""
+    w = W.decode("emu", qh, kvh, 512, lens, page_size=ps, seed=qh + len(lens) + 5)
+    got, over, log = emu.run_decode(w, shared=True, env={"SILVANN_GFX950_DECODE_LATENT": "wide", "EMU_LAUNCHES": "1"})
+    want, _ = oracle.decode_paged(w.q, w.k, w.k, w.pages, w.pages_row, w.page_size, w.k_row, w.lens, qh, kvh, 512,
+                                  w.rows)
+    parity(got, want)
+    assert over == 0
+    assert any("decode_latent" in ln for ln in log.splitlines() if ln.startswith("emu launch ")), log[-500:]
+
+
 FUSED = {"SILVANN_GFX950_DECODE_FUSED": "1"}
 
 

@@ -3,7 +3,9 @@
 - SILVANN_GFX950_DECODE_FUSED=1: the last split of each row and head block merges the others (no merge launch);
 - SILVANN_GFX950_DECODE_INLINE=1: each workgroup makes the plan itself at batches of at most 64 rows (no plan launch);
 - both of those: one launch a step, the finished-split counts tagged with the call's tag instead of cleared;
-- SILVANN_GFX950_DECODE_VTR=1: the V^T operand through the transposing LDS read at head_dim <= 256.
+- SILVANN_GFX950_DECODE_VTR=1: the V^T operand through the transposing LDS read at head_dim <= 256;
+- SILVANN_GFX950_DECODE_LATENT=wide: latent attention (head_dim 512, keys the values) with a workgroup's four waves
+  over four head blocks of one split, sharing its tiles (decode_latent).
 
 A switch is read once a process, so the whole decode suite (tests/test_gpu_decode.py: the oracle, the torch fp32
 reference, zero-length rows, the closed forms, page-table bit-exactness, determinism) runs again in a child process
@@ -27,6 +29,7 @@ SUITES = {   # name: (switches, suites)
     "one-launch": ({"SILVANN_GFX950_DECODE_FUSED": "1", "SILVANN_GFX950_DECODE_INLINE": "1"},
                    ["test_gpu_decode.py", "test_gpu_chains.py"]),
     "vtr": ({"SILVANN_GFX950_DECODE_VTR": "1"}, ["test_gpu_decode.py"]),
+    "latent-wide": ({"SILVANN_GFX950_DECODE_LATENT": "wide"}, ["test_gpu_latent.py"]),
 }
 
 
