@@ -142,7 +142,8 @@ def traffic_for(kernel, workload):
         return None
     try:
         d = json.loads(f.read_text()).get(f"{kernel}:{workload}")
-        return None if d is None else d["traffic_bytes"]
+        # a measurement of an older build of the kernel is not this one's traffic
+        return None if d is None or d.get("older_build") else d["traffic_bytes"]
     except Exception:
         return None
 
