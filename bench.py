@@ -102,9 +102,9 @@ def _flush_l2():
 
 def time_steps(step, steps, warmup, kernel):
     """Warm up, then time exactly `steps` steps, each after a cache flush: the steps' own durations (hipEvents on
-    torch's current stream, which the library is set to launch on, around each step, the flush outside them), the wall clock of the whole
-    timed region between device synchronisations (flushes included), and the named kernel's average launch
-    duration (the library's hipEvents around that kernel)."""
+    torch's current stream, which the library is set to launch on, around each step, the flush outside them), the
+    wall clock of the whole timed region between device synchronisations (flushes included), and the named
+    kernel's average launch duration (the library's hipEvents around that kernel)."""
     import torch
     import silvann_amd
     L = silvann_amd.lib()
