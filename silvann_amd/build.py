@@ -28,13 +28,19 @@ FLAGS = [
 
 
 def _compile(src: Path) -> Path:
+    """One source to its object; hipcc's per-kernel resource report (registers, spills, LDS, occupancy) goes to
+    _build/<object>.resources.txt, where tests/test_resources.py reads it."""
     obj = BUILD / (src.parent.name + "_" + src.stem + ".o" if src.parent != CSRC else src.stem + ".o")
-    cmd = [HIPCC, *FLAGS, "-c", str(src), "-o", str(obj)]
+    cmd = [HIPCC, *FLAGS, "-Rpass-analysis=kernel-resource-usage", "-fno-caret-diagnostics", "-c", str(src), "-o",
+           str(obj)]
     r = subprocess.run(cmd, capture_output=True, text=True)
     noise = "is not a recognized feature for this target"
-    err = "\n".join(line for line in (r.stdout + r.stderr).splitlines() if noise not in line)
+    lines = [line for line in (r.stdout + r.stderr).splitlines() if noise not in line]
+    report = [line for line in lines if "kernel-resource-usage" in line]
+    err = "\n".join(line for line in lines if "kernel-resource-usage" not in line and "remark:" not in line)
     if r.returncode != 0:
         raise RuntimeError(f"hipcc failed on {src.name}:\n{err}")
+    obj.with_suffix(".resources.txt").write_text("\n".join(report) + "\n")
     if err.strip():
         print(err, file=sys.stderr)
     return obj
