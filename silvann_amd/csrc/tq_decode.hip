@@ -64,10 +64,26 @@ template <int D> __device__ __forceinline__ uint64_t codes8(const uint8_t* row, 
     else return *(const uint64_t*)(row + c0);
 }
 
-template <int D> __device__ __forceinline__ f16x8 decode8(uint64_t bits, float scale, const float* lev) {
+// Eight values from their codes: level × the row's scale, rounded once to fp16. D = 8: a level (fp32, from the fp16
+// table) a code. D = 4: a byte of two codes is one read of `lev2`, its two levels as fp16 pair, scaled with one packed
+// fp16 multiply — the same bits, since a product of two fp16 values is exact in fp32 before its one rounding.
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+template <int D> __device__ __forceinline__ f16x8 decode8(uint64_t bits, float scale, const float* lev,
+                                                          const uint32_t* lev2) {
     f16x8 x;
+    if constexpr (D == 4) {
+        const _Float16 sh = (_Float16)scale;   // exact: the scale is an fp16 value
+        const f16x2 s2 = {sh, sh};
 #pragma unroll
-    for (int i = 0; i < 8; ++i) x[i] = (_Float16)(scale * lev[(bits >> (D * i)) & ((1u << D) - 1u)]);
+        for (int b = 0; b < 4; ++b) {
+            const f16x2 v = __builtin_bit_cast(f16x2, lev2[(bits >> (8 * b)) & 0xFFu]) * s2;
+            x[2 * b] = v[0];
+            x[2 * b + 1] = v[1];
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) x[i] = (_Float16)(scale * lev[(bits >> (D * i)) & ((1u << D) - 1u)]);
+    }
     return x;
 }
 
@@ -84,6 +100,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
     constexpr int kSmem = kStageBytes > kMergeBytes ? kStageBytes : kMergeBytes;
     __shared__ __attribute__((aligned(16))) unsigned char smem[kSmem];
     __shared__ float lev[1 << D];
+    __shared__ uint32_t lev2[D == 4 ? 256 : 1];   // D = 4: byte b's two levels, low nibble's in the low half
 
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
     const int col = lane & 15, grp = lane >> 4;
@@ -97,6 +114,9 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
     const int nh = min(16, (int)(a.group - hb * 16));
 
     for (uint32_t c = threadIdx.x; c < (1u << D); c += kThreads) lev[c] = half_bits_to_float(level_bits<D>(c));
+    if constexpr (D == 4)
+        for (uint32_t b = threadIdx.x; b < 256; b += kThreads)
+            lev2[b] = (uint32_t)level_bits<4>(b & 15u) | ((uint32_t)level_bits<4>(b >> 4) << 16);
 
     f16x8 qb[KS];
     {
@@ -140,7 +160,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
         for (int i = 0; i < VCH; ++i) {
             const int slot = lane + 64 * i, key = slot / CPR, c = slot % CPR;
             const uint64_t vrow = (uint64_t)(t0 + (key < (int)nvalid ? key : 0)) * a.kv_heads + g;
-            const f16x8 x = decode8<D>(codes8<D>(a.vc + vrow * rb, 8 * c), half_bits_to_float(a.vs[vrow]), lev);
+            const f16x8 x = decode8<D>(codes8<D>(a.vc + vrow * rb, 8 * c), half_bits_to_float(a.vs[vrow]), lev, lev2);
             *(f16x8*)(vt + (key * CPR + vslot(key, c)) * 8) = x;
         }
 
@@ -150,7 +170,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
             f32x4 st = (f32x4)0.0f;
 #pragma unroll
             for (int ks = 0; ks < KS; ++ks)
-                st = __builtin_amdgcn_mfma_f32_16x16x32_f16(decode8<D>(kcodes[p][ks], kscale[p], lev), qb[ks], st, 0, 0, 0);
+                st = __builtin_amdgcn_mfma_f32_16x16x32_f16(decode8<D>(kcodes[p][ks], kscale[p], lev, lev2), qb[ks], st, 0, 0, 0);
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
                 const int key = 16 * p + 4 * grp + r;
