@@ -26,7 +26,8 @@ and an 8-bit tier of C5's shape, in GB/s of codes, scales, q and residuals; the 
 (attention_cache_write_paged) placing C4's 2,048-row chunk, keys turned, in GB/s; GLM 5.3's latent attention
 (64 heads over 131,072 512-wide latents, row 137 with k = v) in GB/s with its TFLOP/s beside; and C5 / C3
 through the reference's own decode and rows verbs, whose door chains this library defers and runs fused. With
-`--variants`, C2 once more with each of the split-K decode's opt-in forms.
+`--variants`, C2 once more with each of the split-K decode's opt-in forms, and C3 and C4 with each opt-in prefill
+kernel (causal_duo, causal_pipe).
 
 `cpu_baseline` is the reference's own x86_avx2 silicon family (oracle/_ref, built from the reference's
 sources) over the same batch, its doors called through its nn table on the host cores — both of the
@@ -63,7 +64,7 @@ def parse():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--variants", action="store_true",
                     help="also the decode's opt-in candidates (fused finish, transposing reads, inline plan, one "
-                         "launch) as child-process lines")
+                         "launch) and the prefill's (causal_duo, causal_pipe) as child-process lines")
     ap.add_argument("--extra", action="store_true",
                     help="also the lines of the section-f rows and the reference verbs (--only 6..11) as child processes")
     ap.add_argument("--cpu-threads", type=int, default=int(os.environ.get("BENCH_CPU_THREADS", "16")))
@@ -482,6 +483,11 @@ def main():
                                       variant="one launch a step (inline plan + fused finish)"))
             secondary.append(isolated(9, max(5, a.steps // 2), a.warmup, env={"SILVANN_GFX950_DECODE_LATENT": "wide"},
                                       variant="latent attention, four head blocks a workgroup (decode_latent)"))
+            for kernel, what in (("duo", "causal_duo: two waves a SIMD over alternate key tiles"),
+                                 ("pipe", "causal_pipe: one wave a SIMD, pipelined two tiles deep")):
+                for n in (3, 4):
+                    secondary.append(isolated(n, max(3, a.steps // 4), min(a.warmup, 2),
+                                              env={"SILVANN_GFX950_PREFILL": kernel}, variant=what))
             for n in (1, 5):   # the launch-bound and the longest decode in one launch
                 secondary.append(isolated(n, max(5, a.steps // 2), a.warmup,
                                           env={"SILVANN_GFX950_DECODE_INLINE": "1", "SILVANN_GFX950_DECODE_FUSED": "1"},

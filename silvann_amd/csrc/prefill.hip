@@ -830,6 +830,241 @@ __global__ __launch_bounds__(kThreads) void causal_pipe(CausalArgs a) {
     if (hit) *a.over = kFaultOverflow;
 }
 
+
+// ── causal_duo: two waves a SIMD, each taking every other key tile ─────────────────────────────────────
+//
+// causal_mfma runs one wave a SIMD: a wave's softmax and every wait on its operands leave the matrix cores
+// idle, since no other wave on the SIMD has MFMAs to issue. causal_duo gives each (query head, 32 rows) two
+// waves, on the same SIMD (waves w and w + 4), which take the even and the odd key tiles: while one waits or
+// runs its exponentials the other's MFMAs go to the matrix cores. A workgroup is 8 waves: 4 query heads of
+// one kv head's group over the same 32 rows, so a K/V tile in LDS still serves four heads. The ring holds
+// two pairs of tiles: pair j (tiles 2j, 2j + 1) is read while pair j + 1 lands, one barrier a pair. Each
+// wave keeps its own running max, sum and O^T; at the end the two waves of a head exchange halves of O^T
+// through LDS (the ring's bytes, free by then) and each merges and writes half the head dims:
+//   m = max(m0, m1),  l = l0·2^(m0 − m) + l1·2^(m1 − m),  O = (O0·2^(m0 − m) + O1·2^(m1 − m)) / l
+// — the reference's merge of two residuals (kernels.cuh:1243-1267) in base 2. The register budget is half
+// causal_mfma's (256 a lane: O^T's 128 in accumulation registers, Q^T's 64 and the tile's scores, weights
+// and operands in the rest), so there is no read-ahead of a next tile's scores.
+constexpr int kDuoWaves = 8;
+constexpr int kDuoThreads = 64 * kDuoWaves;
+
+template <int HD, bool PAIRED, bool PTL>
+__global__ __launch_bounds__(kDuoThreads) void causal_duo(CausalArgs a) {
+    static_assert(HD == 128 || HD == 256, "a tile's loads split evenly over 512 threads");
+    constexpr int CPR = HD / 8;
+    constexpr int KSTEPS = HD / 16;
+    constexpr int DT = HD / 32;
+    constexpr int LOADS = kKT * CPR / kDuoThreads;
+    constexpr uint32_t RB = 2 * HD;
+    __shared__ __attribute__((aligned(16))) Stage<HD> ring[kStages];
+    __shared__ uint32_t pt[PTL ? kPagesInLds : 1];
+    __shared__ float ml[kDuoWaves][2][64];   // the merge: each wave's running max and sum, a lane each
+    static_assert(sizeof(ring) == kDuoWaves * (DT / 2) * 16 * 64 * sizeof(float), "the exchange fills the ring");
+
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int hi = w & 3, par = w >> 2;   // head of the workgroup's four; tile parity
+    const int col = lane & 31, half = lane >> 5;
+    const Block blk = xcd_block();
+    const uint32_t g = blk.y / a.hblocks, hb = blk.y % a.hblocks;
+    const uint32_t head = g * a.group + hb * 4 + hi;
+    const uint32_t row = a.kv_heads * HD;
+    bool hit = false;
+
+    uint32_t koff[LOADS], voff[LOADS];
+#pragma unroll
+    for (int i = 0; i < LOADS; ++i) {
+        const int s = tid + kDuoThreads * i, r = s / CPR, pc = s % CPR;
+        koff[i] = (uint32_t)r * row * 2u + 16u * kslot<CPR>(r, pc);
+        voff[i] = (uint32_t)r * row * 2u + 16u * vslot<CPR>(r, pc);
+    }
+    // The operand reads' LDS offsets, one register each: the swizzles touch chunk bits the k-step (K: bits 1-3
+    // of the chunk) or the dim tile (V: bits 2-3) sets, so k-step kk's offset is kread ^ 32·(kk % 8) (+ 256 for
+    // kk >= 8, an immediate) and dim tile n's is vread ^ 64·(n % 4) (+ 256 for n >= 4).
+    static_assert(CPR >= 16, "the k-step and dim-tile bits are below the swizzle's reach");
+    uint32_t kread, vread;
+    {
+        const int b16 = lane >> 4, li = lane & 15, jj = li >> 2, rr = li & 3, key = 4 * half + jj;
+        kread = col * RB + 16u * kslot<CPR>(col, half);
+        const int d0 = 16 * (b16 & 1) + 4 * rr;
+        vread = key * RB + 16u * vslot<CPR>(key, d0 >> 3) + 2u * (d0 & 7);
+    }
+
+    f32x16 acc[DT];
+    f16x8 qb[KSTEPS];
+
+    auto process = [&](uint32_t rtile) __attribute__((always_inline)) {
+        const uint32_t r0 = rtile * 32;
+        const uint32_t rlast = min(a.rows, r0 + 32) - 1;
+        const uint32_t nkeys = a.first + rlast + 1;
+        const uint32_t ntiles = (nkeys + kKT - 1) / kKT;
+        const uint32_t myrow = r0 + col;
+        const bool row_ok = myrow < a.rows;
+        {
+            const uint16_t* qr = a.q + ((uint64_t)(row_ok ? myrow : 0) * a.q_heads + head) * HD;
+#pragma unroll
+            for (int kk = 0; kk < KSTEPS; ++kk) qb[kk] = *(const f16x8*)(qr + 16 * kk + 8 * half);
+        }
+        const uint32_t mypos = a.first + (row_ok ? myrow : 0);
+        const uint32_t diag_from = a.first + r0;
+#pragma unroll
+        for (int n = 0; n < DT; ++n) acc[n] = (f32x16)0.0f;
+        float m = -INFINITY, l = 0.0f;
+
+        uint32_t lt = 0, lj = 0, loff = 0, page = 0;
+        auto load_tile = [&]() __attribute__((always_inline)) {
+            uint64_t base;
+            if (!a.pages) {
+                base = (uint64_t)lt * kKT * row;
+            } else {
+                if (loff == 0) {
+                    if constexpr (PTL) page = __builtin_amdgcn_readfirstlane(pt[lj]);
+                    else page = scalar_load(a.pages + lj);
+                }
+                base = ((uint64_t)page * a.page_size + loff) * row;
+                loff += kKT;
+                if (loff == a.page_size) { loff = 0; ++lj; }
+            }
+            base += (uint64_t)g * HD;
+            const bool full = (lt + 1) * kKT <= nkeys;
+            char* S = (char*)&ring[lt % kStages];
+            const uint32_t left = nkeys - lt * kKT;
+            ++lt;
+            const uint16_t* kb = a.k + base;
+            const uint16_t* vb = a.v + base;
+#pragma unroll
+            for (int i = 0; i < LOADS; ++i) {
+                const uint32_t at = 16u * (kDuoThreads * i + (tid & ~63));
+                // the last tile: keys past the cache bring the tile's key 0 (masked)
+                const uint32_t r = (uint32_t)(tid + kDuoThreads * i) / CPR, back = full || r < left ? 0u : r * row * 2u;
+                dma16s(kb, koff[i] - back, (lds_ptr)(S + at));
+                dma16s(vb, voff[i] - back, (lds_ptr)(S + sizeof(_Float16) * kKT * HD + at));
+            }
+        };
+
+        __syncthreads();   // the ring, the page table and the exchange area are free
+        if (PTL && a.pages) {
+            const uint32_t npages = (nkeys + a.page_size - 1) / a.page_size;
+            for (uint32_t j = tid; j < npages; j += kDuoThreads) pt[j] = a.pages[j];
+            __builtin_amdgcn_s_waitcnt(0x0F70);
+            __syncthreads();
+        }
+        load_tile();
+        if (ntiles > 1) load_tile();
+
+        for (uint32_t t0 = 0; t0 < ntiles; t0 += 2) {
+            __builtin_amdgcn_s_waitcnt(0x0F70);   // this thread's part of pair t0 / 2 landed
+            __syncthreads();                      // everyone's has; pair t0 / 2 - 1's stages are free
+            if (t0 + 2 < ntiles) load_tile();
+            if (t0 + 3 < ntiles) load_tile();
+            const uint32_t t = t0 + par;
+            if (t >= ntiles) continue;   // the odd wave of a last, lone tile
+            const int st = t % kStages;
+            // S^T (32 keys × 32 rows): lane holds keys 8·(r/4) + 4·half + r%4 of row col
+            f32x16 c = (f32x16)0.0f;
+            {
+                const char* S = (const char*)ring[st].k;
+#pragma unroll
+                for (int kk = 0; kk < KSTEPS; ++kk)
+                    c = __builtin_amdgcn_mfma_f32_32x32x16_f16(*(const f16x8*)(S + (kread ^ (32u * (kk % 8))) + 256 * (kk / 8)),
+                                                                qb[kk], c, 0, 0, 0);
+            }
+            if (t * kKT + kKT - 1 > diag_from) {
+                const int lim = (int)(mypos - t * kKT) - 4 * half;
+#pragma unroll
+                for (int r = 0; r < 16; ++r) c[r] = 8 * (r / 4) + (r % 4) > lim ? -INFINITY : c[r];
+            }
+            float x = c[0];
+#pragma unroll
+            for (int r = 1; r < 16; ++r) x = fmaxf(x, c[r]);
+            const float mx = max_xor32(x) * a.scale_log2;
+            if (__builtin_amdgcn_ballot_w64(mx > m + kRescale)) {   // the lazy rescale of causal_mfma
+                const float mnew = fmaxf(m, mx);
+                const float corr = __builtin_amdgcn_exp2f(m - mnew);
+                l *= corr;
+#pragma unroll
+                for (int n = 0; n < DT; ++n) acc[n] *= corr;
+                m = mnew;
+            }
+            float lsum = 0.0f;
+            f16x8 pb[2];
+            const float nm = -m;
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const float p = __builtin_amdgcn_exp2f(fmaf(c[r], a.scale_log2, nm));
+                lsum += p;
+                pb[r / 8][r % 8] = (_Float16)p;
+            }
+            l += lsum;
+            // O^T += V^T · P^T, V^T through the transposing LDS read (as causal_mfma's mix)
+            const char* S = (const char*)ring[st].v;
+#pragma unroll
+            for (int s2 = 0; s2 < 2; ++s2)
+#pragma unroll
+                for (int n = 0; n < DT; ++n) {
+                    const s16x4 x0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                        (__attribute__((address_space(3))) s16x4*)(S + (vread ^ (64u * (n % 4))) + 256 * (n / 4) + (16 * s2) * RB));
+                    const s16x4 x1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                        (__attribute__((address_space(3))) s16x4*)(S + (vread ^ (64u * (n % 4))) + 256 * (n / 4) +
+                                                                   (16 * s2 + 8) * RB));
+                    const f16x8 va = __builtin_bit_cast(f16x8, __builtin_shufflevector(x0, x1, 0, 1, 2, 3, 4, 5, 6, 7));
+                    acc[n] = __builtin_amdgcn_mfma_f32_32x32x16_f16(va, pb[s2], acc[n], 0, 0, 0);
+                }
+        }
+
+        // The merge. Wave par keeps dim tiles [par·DT/2, par·DT/2 + DT/2) and hands the other half to its partner
+        // (wave w ^ 4) through the ring's bytes: exchange slot (wave, tile, register) holds 64 lanes' floats.
+        l = sum_xor32(l);
+        __syncthreads();   // every wave is done with the ring
+        float* X = (float*)ring;
+        const int pw = w ^ 4;
+        ml[w][0][lane] = m;
+        ml[w][1][lane] = l;
+        // Which half a wave keeps is chosen by value, tile by tile (par is wave-uniform): an index or a branch on
+        // par would let the compiler address O^T in memory, putting it in scratch.
+#pragma unroll
+        for (int n = 0; n < DT / 2; ++n) {
+            const f32x16 gv = par ? acc[n] : acc[n + DT / 2];
+#pragma unroll
+            for (int i = 0; i < 16; ++i) X[((w * (DT / 2) + n) * 16 + i) * 64 + lane] = gv[i];
+        }
+        __syncthreads();
+        const float m1 = ml[pw][0][lane], l1 = ml[pw][1][lane];
+        const float mm = fmaxf(m, m1);
+        const float c0 = __builtin_amdgcn_exp2f(m - mm), c1 = __builtin_amdgcn_exp2f(m1 - mm);
+        const float inv_l = 1.0f / (l * c0 + l1 * c1);
+        if (!row_ok) return;
+        const float a0 = c0 * inv_l, a1 = c1 * inv_l;
+        uint16_t* orow = a.o + ((uint64_t)myrow * a.q_heads + head) * HD + par * (HD / 2);
+#pragma unroll
+        for (int n = 0; n < DT / 2; ++n) {
+            const f32x16 kv = par ? acc[n + DT / 2] : acc[n];
+#pragma unroll
+            for (int qd = 0; qd < 4; ++qd) {
+                // register 4·qd + i holds dim 32·n' + 8·qd + 4·half + i of dim tile n'
+                uint16_t hv[4];
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const float o1 = X[((pw * (DT / 2) + n) * 16 + 4 * qd + i) * 64 + lane];
+                    hv[i] = to_half(kv[4 * qd + i] * a0 + o1 * a1, hit);
+                }
+                const uint64_t packed = (uint64_t)hv[0] | ((uint64_t)hv[1] << 16) | ((uint64_t)hv[2] << 32) |
+                                        ((uint64_t)hv[3] << 48);
+                *(uint64_t*)(orow + 32 * n + 8 * qd + 4 * half) = packed;
+            }
+        }
+    };
+
+    if (PAIRED) {
+        const uint32_t heavy = a.rtiles - 1 - blk.x, light = blk.x;
+        process(heavy);
+        if (light < heavy) process(light);
+    } else {
+        process(a.rtiles - 1 - blk.x);
+    }
+    if (hit) *a.over = kFaultOverflow;
+}
+
 }  // namespace
 
 // Which head_dim-256 kernel runs: causal_mfma (the default) or causal_pipe, chosen once a process by
@@ -839,6 +1074,15 @@ static bool prefill_pipe() {
     static const bool on = [] {
         const char* e = getenv("SILVANN_GFX950_PREFILL");
         return e && strcmp(e, "pipe") == 0;
+    }();
+    return on;
+}
+// causal_duo (two waves a SIMD) for the fp16 answers at head_dim 128 and 256 when the group is a multiple of 4,
+// chosen by SILVANN_GFX950_PREFILL=duo; checked in the CPU emulation, not yet timed on a GPU.
+static bool prefill_duo() {
+    static const bool on = [] {
+        const char* e = getenv("SILVANN_GFX950_PREFILL");
+        return e && strcmp(e, "duo") == 0;
     }();
     return on;
 }
@@ -901,7 +1145,19 @@ void causal_paged_launch(uint16_t* o, float* res, const uint16_t* q, const uint1
         if (ptl) causal_mfma<HDV, false, true><<<grid, kThreads, 0, st>>>(a); \
         else causal_mfma<HDV, false, false><<<grid, kThreads, 0, st>>>(a); \
     }
-    if (res) {
+    if (!res && prefill_duo() && a.hw == 4 && head_dim >= 128) {
+        const dim3 g2 = grid;
+#define SILVANN_CAUSAL_DUO(HDV) \
+    if (paired) { \
+        if (ptl) causal_duo<HDV, true, true><<<g2, kDuoThreads, 0, st>>>(a); \
+        else causal_duo<HDV, true, false><<<g2, kDuoThreads, 0, st>>>(a); \
+    } else { \
+        if (ptl) causal_duo<HDV, false, true><<<g2, kDuoThreads, 0, st>>>(a); \
+        else causal_duo<HDV, false, false><<<g2, kDuoThreads, 0, st>>>(a); \
+    }
+        if (head_dim == 128) { SILVANN_CAUSAL_DUO(128) } else { SILVANN_CAUSAL_DUO(256) }
+#undef SILVANN_CAUSAL_DUO
+    } else if (res) {
         switch (head_dim) {
             case 64: SILVANN_CAUSAL_RES(64) break;
             case 128: SILVANN_CAUSAL_RES(128) break;

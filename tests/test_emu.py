@@ -20,6 +20,7 @@ from tests.emu import emu
 pytestmark = pytest.mark.skipif(emu.compiler() is None, reason="no clang++ for the CPU emulation")
 
 PIPE = {"SILVANN_GFX950_PREFILL": "pipe"}
+DUO = {"SILVANN_GFX950_PREFILL": "duo"}
 
 
 def _causal(oracle, hd, qh, kvh, first, rows, ps, env=None):
@@ -46,6 +47,17 @@ def test_causal_default_kernel(oracle, hd, qh, kvh, first, rows, ps):
 ])
 def test_causal_pipe_kernel(oracle, hd, qh, kvh, first, rows, ps):
     _causal(oracle, hd, qh, kvh, first, rows, ps, env=PIPE)
+
+
+@pytest.mark.parametrize("hd,qh,kvh,first,rows,ps", [
+    (256, 16, 2, 0, 130, 0),     # paired row tiles; an odd tile count leaves the odd waves a lone last tile
+    (256, 8, 2, 37, 90, 64),     # paged, page table in LDS; a prefix longer than a tile
+    (128, 4, 1, 300, 40, 32),    # unpaired (prefix past the chunk); 32-position pages
+    (128, 8, 1, 5, 1, 0),        # one row: one tile, the odd waves idle; the merge over an empty partner
+])
+def test_causal_duo_kernel(oracle, hd, qh, kvh, first, rows, ps):
+    """causal_duo (two waves a SIMD over alternate key tiles, merged through LDS) against the oracle."""
+    _causal(oracle, hd, qh, kvh, first, rows, ps, env=DUO)
 
 
 @pytest.mark.parametrize("qh,kvh,hd,lens,ps", [

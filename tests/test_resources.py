@@ -49,6 +49,7 @@ def test_no_scratch_spills_and_lds_within_a_cu(report):
     (r"decode_latentI", 1),
     (r"causal_mfmaI", 1),
     (r"causal_pipeI", 1),
+    (r"causal_duoI", 2),                    # two waves a SIMD is the design of causal_duo
 ])
 def test_occupancy(report, pattern, waves):
     hits = {n: r for n, r in report.items() if re.search(pattern, n)}
