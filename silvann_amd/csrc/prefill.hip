@@ -980,7 +980,8 @@ __global__ __launch_bounds__(kDuoThreads) void causal_duo(CausalArgs a) {
             const float mx = max_xor32(x) * a.scale_log2;
             if (__builtin_amdgcn_ballot_w64(mx > m + kRescale)) {   // the lazy rescale of causal_mfma
                 const float mnew = fmaxf(m, mx);
-                const float corr = __builtin_amdgcn_exp2f(m - mnew);
+                // a row that has still seen no key (m and mnew -inf) keeps its zeros
+                const float corr = mnew == -INFINITY ? 1.0f : __builtin_amdgcn_exp2f(m - mnew);
                 l *= corr;
 #pragma unroll
                 for (int n = 0; n < DT; ++n) acc[n] *= corr;
@@ -988,7 +989,10 @@ __global__ __launch_bounds__(kDuoThreads) void causal_duo(CausalArgs a) {
             }
             float lsum = 0.0f;
             f16x8 pb[2];
-            const float nm = -m;
+            // A row may have seen no key yet: the odd wave's first tile can lie wholly past a row's position (the
+            // even wave's tile 0 always holds key 0). Its max is still -inf; its weights must be 0, not
+            // 2^(-inf + inf), and a rescale that other rows of the wave ask for must leave it at 0 (above).
+            const float nm = m == -INFINITY ? 0.0f : -m;
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
                 const float p = __builtin_amdgcn_exp2f(fmaf(c[r], a.scale_log2, nm));

@@ -54,6 +54,7 @@ def test_causal_pipe_kernel(oracle, hd, qh, kvh, first, rows, ps):
     (256, 8, 2, 37, 90, 64),     # paged, page table in LDS; a prefix longer than a tile
     (128, 4, 1, 300, 40, 32),    # unpaired (prefix past the chunk); 32-position pages
     (128, 8, 1, 5, 1, 0),        # one row: one tile, the odd waves idle; the merge over an empty partner
+    (256, 8, 2, 1, 33, 96),      # the odd waves' first tile past most rows' positions: rows with no key seen yet
 ])
 def test_causal_duo_kernel(oracle, hd, qh, kvh, first, rows, ps):
     """causal_duo (two waves a SIMD over alternate key tiles, merged through LDS) against the oracle."""

@@ -105,3 +105,20 @@ def test_tq(oracle, seed):
     np.testing.assert_allclose(got[:, 1:2] * at, want[:, 1:2], rtol=2e-3)
     fin = lambda r: (r[:, 2:] / r[:, 1:2]).astype(np.float16)  # noqa: E731
     parity(fin(got), fin(want))
+
+
+@pytest.mark.parametrize("seed", range(10))
+def test_causal_duo(oracle, seed):
+    """SILVANN_GFX950_PREFILL=duo over random shapes: groups of 4 and 8 take causal_duo at head_dim 128 and 256;
+    other groups and widths fall back to causal_mfma under the same switch."""
+    rng = random.Random(400 + seed)
+    hd = rng.choice([128, 256, 256, 64])
+    kvh = rng.choice([1, 2])
+    qh = kvh * rng.choice([4, 8, 8, 2])
+    first, rows, ps = rng.choice([0, 1, 33, 300]), rng.choice([1, 31, 33, 97, 130]), rng.choice([0, 32, 64, 96])
+    print(f"case: causal duo qh{qh} kvh{kvh} hd{hd} first{first} rows{rows} ps{ps}", flush=True)
+    w = W.causal("rand", qh, kvh, hd, first, rows, page_size=ps, seed=400 + seed)
+    got, over, _ = emu.run_causal(w, {"SILVANN_GFX950_PREFILL": "duo"})
+    want, _ = oracle.causal_rows(w.q, w.k, w.v, w.pages, w.page_size, qh, kvh, hd, first, list(range(rows)))
+    parity(got, want)
+    assert over == 0
