@@ -22,6 +22,14 @@ GPU_FIRST = ("test_gpu_decode.py", "test_gpu_doors.py", "test_gpu_prefill.py")
 GPU_LAST = ("test_gpu_decode_variants.py",)
 
 
+# GPU suites whose kernels have never run on an MI355X (checked only in the CPU emulation of tests/emu). A first run
+# of a new kernel can fault the GPU and end the process, and with it every result of the session, so these are
+# skipped unless SILVANN_GPU_UNVERIFIED=1: a builder's session runs each of them once, on its own, and a suite
+# leaves this list when it has passed there.
+GPU_UNVERIFIED = ("test_gpu_tq.py", "test_gpu_window.py", "test_gpu_cache.py", "test_gpu_latent.py",
+                  "test_gpu_chains.py", "test_gpu_family.py", "test_gpu_softmax_sink.py", "test_gpu_rows_pairs.py",
+                  "test_gpu_decode_variants.py")
+
 _current = {"test": "(collecting)"}
 
 
@@ -63,6 +71,12 @@ def pytest_collection_modifyitems(config, items):
             return GPU_FIRST.index(name)
         return len(GPU_FIRST) + (1 + GPU_LAST.index(name) if name in GPU_LAST else 0)
     items[:] = sorted(items, key=rank)
+    if os.environ.get("SILVANN_GPU_UNVERIFIED") != "1":
+        skip = pytest.mark.skip(reason="kernels not yet run on an MI355X (CPU emulation only): run this suite once "
+                                       "with SILVANN_GPU_UNVERIFIED=1")
+        for item in items:
+            if Path(str(item.fspath)).name in GPU_UNVERIFIED:
+                item.add_marker(skip)
 
 
 @pytest.fixture(scope="session")
