@@ -44,6 +44,12 @@ namespace {
 #ifndef SILVANN_PREFILL_UNIFORM_WAVE
 #define SILVANN_PREFILL_UNIFORM_WAVE 0
 #endif
+#ifndef SILVANN_DUO_KA   // causal_duo's operand read-ahead in MFMAs (-D in experiment builds; deeper spills at head_dim 256)
+#define SILVANN_DUO_KA 1
+#endif
+#ifndef SILVANN_DUO_VA
+#define SILVANN_DUO_VA 1
+#endif
 #ifndef SILVANN_PREFILL_XCD_ORDER   // 0: workgroups in launch order (an experiment build's comparison)
 #define SILVANN_PREFILL_XCD_ORDER 1
 #endif
@@ -961,13 +967,23 @@ __global__ __launch_bounds__(kDuoThreads) void causal_duo(CausalArgs a) {
             if (t >= ntiles) continue;   // the odd wave of a last, lone tile
             const int st = t % kStages;
             // S^T (32 keys × 32 rows): lane holds keys 8·(r/4) + 4·half + r%4 of row col
+            // operands read KA (K) and VA (V^T) MFMAs ahead into rotating registers, the groups pinned in order
+            constexpr int KA = SILVANN_DUO_KA, VA = SILVANN_DUO_VA;
             f32x16 c = (f32x16)0.0f;
             {
                 const char* S = (const char*)ring[st].k;
+                auto kread_at = [&](int kk) __attribute__((always_inline)) {
+                    return *(const f16x8*)(S + (kread ^ (32u * (kk % 8))) + 256 * (kk / 8));
+                };
+                f16x8 kb[KA + 1];
 #pragma unroll
-                for (int kk = 0; kk < KSTEPS; ++kk)
-                    c = __builtin_amdgcn_mfma_f32_32x32x16_f16(*(const f16x8*)(S + (kread ^ (32u * (kk % 8))) + 256 * (kk / 8)),
-                                                                qb[kk], c, 0, 0, 0);
+                for (int kk = 0; kk < KA; ++kk) kb[kk] = kread_at(kk);
+#pragma unroll
+                for (int kk = 0; kk < KSTEPS; ++kk) {
+                    if (kk + KA < KSTEPS) kb[(kk + KA) % (KA + 1)] = kread_at(kk + KA);
+                    c = __builtin_amdgcn_mfma_f32_32x32x16_f16(kb[kk % (KA + 1)], qb[kk], c, 0, 0, 0);
+                    __builtin_amdgcn_sched_barrier(0);
+                }
             }
             if (t * kKT + kKT - 1 > diag_from) {
                 const int lim = (int)(mypos - t * kKT) - 4 * half;
@@ -1000,20 +1016,27 @@ __global__ __launch_bounds__(kDuoThreads) void causal_duo(CausalArgs a) {
                 pb[r / 8][r % 8] = (_Float16)p;
             }
             l += lsum;
-            // O^T += V^T · P^T, V^T through the transposing LDS read (as causal_mfma's mix)
+            // O^T += V^T · P^T, V^T through the transposing LDS read (as causal_mfma's mix); MFMA i is k-step i / DT,
+            // dim tile i % DT
             const char* S = (const char*)ring[st].v;
+            auto vread_at = [&](int i) __attribute__((always_inline)) {
+                const int s2 = i / DT, n = i % DT;
+                const s16x4 x0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                    (__attribute__((address_space(3))) s16x4*)(S + (vread ^ (64u * (n % 4))) + 256 * (n / 4) + (16 * s2) * RB));
+                const s16x4 x1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                    (__attribute__((address_space(3))) s16x4*)(S + (vread ^ (64u * (n % 4))) + 256 * (n / 4) +
+                                                               (16 * s2 + 8) * RB));
+                return __builtin_bit_cast(f16x8, __builtin_shufflevector(x0, x1, 0, 1, 2, 3, 4, 5, 6, 7));
+            };
+            f16x8 vb[VA + 1];
 #pragma unroll
-            for (int s2 = 0; s2 < 2; ++s2)
+            for (int i = 0; i < VA; ++i) vb[i] = vread_at(i);
 #pragma unroll
-                for (int n = 0; n < DT; ++n) {
-                    const s16x4 x0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-                        (__attribute__((address_space(3))) s16x4*)(S + (vread ^ (64u * (n % 4))) + 256 * (n / 4) + (16 * s2) * RB));
-                    const s16x4 x1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-                        (__attribute__((address_space(3))) s16x4*)(S + (vread ^ (64u * (n % 4))) + 256 * (n / 4) +
-                                                                   (16 * s2 + 8) * RB));
-                    const f16x8 va = __builtin_bit_cast(f16x8, __builtin_shufflevector(x0, x1, 0, 1, 2, 3, 4, 5, 6, 7));
-                    acc[n] = __builtin_amdgcn_mfma_f32_32x32x16_f16(va, pb[s2], acc[n], 0, 0, 0);
-                }
+            for (int i = 0; i < 2 * DT; ++i) {
+                if (i + VA < 2 * DT) vb[(i + VA) % (VA + 1)] = vread_at(i + VA);
+                acc[i % DT] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vb[i % (VA + 1)], pb[i / DT], acc[i % DT], 0, 0, 0);
+                __builtin_amdgcn_sched_barrier(0);
+            }
         }
 
         // The merge. Wave par keeps dim tiles [par·DT/2, par·DT/2 + DT/2) and hands the other half to its partner
