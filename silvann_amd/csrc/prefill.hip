@@ -50,6 +50,9 @@ namespace {
 #ifndef SILVANN_DUO_VA
 #define SILVANN_DUO_VA 1
 #endif
+#ifndef SILVANN_DUO_PIN   // 0: the compiler schedules causal_duo's operand reads (an experiment build's comparison)
+#define SILVANN_DUO_PIN 1
+#endif
 #ifndef SILVANN_PREFILL_XCD_ORDER   // 0: workgroups in launch order (an experiment build's comparison)
 #define SILVANN_PREFILL_XCD_ORDER 1
 #endif
@@ -982,7 +985,7 @@ __global__ __launch_bounds__(kDuoThreads) void causal_duo(CausalArgs a) {
                 for (int kk = 0; kk < KSTEPS; ++kk) {
                     if (kk + KA < KSTEPS) kb[(kk + KA) % (KA + 1)] = kread_at(kk + KA);
                     c = __builtin_amdgcn_mfma_f32_32x32x16_f16(kb[kk % (KA + 1)], qb[kk], c, 0, 0, 0);
-                    __builtin_amdgcn_sched_barrier(0);
+                    if constexpr (SILVANN_DUO_PIN != 0) __builtin_amdgcn_sched_barrier(0);
                 }
             }
             if (t * kKT + kKT - 1 > diag_from) {
@@ -1035,7 +1038,7 @@ __global__ __launch_bounds__(kDuoThreads) void causal_duo(CausalArgs a) {
             for (int i = 0; i < 2 * DT; ++i) {
                 if (i + VA < 2 * DT) vb[(i + VA) % (VA + 1)] = vread_at(i + VA);
                 acc[i % DT] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vb[i % (VA + 1)], pb[i / DT], acc[i % DT], 0, 0, 0);
-                __builtin_amdgcn_sched_barrier(0);
+                if constexpr (SILVANN_DUO_PIN != 0) __builtin_amdgcn_sched_barrier(0);
             }
         }
 
