@@ -1152,7 +1152,9 @@ void causal_paged_launch(uint16_t* o, float* res, const uint16_t* q, const uint1
     // pair row tiles when the causal part dominates the work (a prefix shorter than the chunk)
     const bool paired = first < rows && a.rtiles > 1;
     const dim3 grid(paired ? (a.rtiles + 1) / 2 : a.rtiles, a.kv_heads * a.hblocks);
-    if ((uint64_t)grid.x * grid.y * kThreads >= (1ull << 32) || grid.y > 65535) {   // work-items below 2^32
+    const bool duo = !res && prefill_duo() && a.hw == 4 && head_dim >= 128;
+    const uint64_t threads = duo ? kDuoThreads : kThreads;
+    if ((uint64_t)grid.x * grid.y * threads >= (1ull << 32) || grid.y > 65535) {   // work-items below 2^32
         refuse(what);
         return;
     }
@@ -1175,7 +1177,7 @@ void causal_paged_launch(uint16_t* o, float* res, const uint16_t* q, const uint1
         if (ptl) causal_mfma<HDV, false, true><<<grid, kThreads, 0, st>>>(a); \
         else causal_mfma<HDV, false, false><<<grid, kThreads, 0, st>>>(a); \
     }
-    if (!res && prefill_duo() && a.hw == 4 && head_dim >= 128) {
+    if (duo) {
         const dim3 g2 = grid;
 #define SILVANN_CAUSAL_DUO(HDV) \
     if (paired) { \
