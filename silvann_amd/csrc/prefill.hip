@@ -857,7 +857,8 @@ __global__ __launch_bounds__(kThreads) void causal_pipe(CausalArgs a) {
 constexpr int kDuoWaves = 8;
 constexpr int kDuoThreads = 64 * kDuoWaves;
 
-template <int HD, bool PAIRED, bool PTL>
+// RES: each row's residual {m, l, acc} (row 140) in place of its fp16 answer, as causal_mfma<…, RES>.
+template <int HD, bool PAIRED, bool PTL, bool RES = false>
 __global__ __launch_bounds__(kDuoThreads) void causal_duo(CausalArgs a) {
     static_assert(HD == 128 || HD == 256, "a tile's loads split evenly over 512 threads");
     constexpr int CPR = HD / 8;
@@ -867,7 +868,7 @@ __global__ __launch_bounds__(kDuoThreads) void causal_duo(CausalArgs a) {
     constexpr uint32_t RB = 2 * HD;
     __shared__ __attribute__((aligned(16))) Stage<HD> ring[kStages];
     __shared__ uint32_t pt[PTL ? kPagesInLds : 1];
-    __shared__ float ml[kDuoWaves][2][64];   // the merge: each wave's running max and sum, a lane each
+    __shared__ float ml[kDuoWaves][3][64];   // the merge: each wave's running max, sum and (RES) true max
     static_assert(sizeof(ring) == kDuoWaves * (DT / 2) * 16 * 64 * sizeof(float), "the exchange fills the ring");
 
     const int tid = threadIdx.x, lane = tid & 63;
@@ -919,6 +920,7 @@ __global__ __launch_bounds__(kDuoThreads) void causal_duo(CausalArgs a) {
 #pragma unroll
         for (int n = 0; n < DT; ++n) acc[n] = (f32x16)0.0f;
         float m = -INFINITY, l = 0.0f;
+        float mt = -INFINITY;   // RES: the row's true running max (m lags it by up to kRescale)
 
         uint32_t lt = 0, lj = 0, loff = 0, page = 0;
         auto load_tile = [&]() __attribute__((always_inline)) {
@@ -997,6 +999,7 @@ __global__ __launch_bounds__(kDuoThreads) void causal_duo(CausalArgs a) {
 #pragma unroll
             for (int r = 1; r < 16; ++r) x = fmaxf(x, c[r]);
             const float mx = max_xor32(x) * a.scale_log2;
+            if constexpr (RES) mt = fmaxf(mt, mx);
             if (__builtin_amdgcn_ballot_w64(mx > m + kRescale)) {   // the lazy rescale of causal_mfma
                 const float mnew = fmaxf(m, mx);
                 // a row that has still seen no key (m and mnew -inf) keeps its zeros
@@ -1050,6 +1053,7 @@ __global__ __launch_bounds__(kDuoThreads) void causal_duo(CausalArgs a) {
         const int pw = w ^ 4;
         ml[w][0][lane] = m;
         ml[w][1][lane] = l;
+        ml[w][2][lane] = mt;
         // Which half a wave keeps is chosen by value, tile by tile (par is wave-uniform): an index or a branch on
         // par would let the compiler address O^T in memory, putting it in scratch.
 #pragma unroll
@@ -1060,6 +1064,29 @@ __global__ __launch_bounds__(kDuoThreads) void causal_duo(CausalArgs a) {
         }
         __syncthreads();
         const float m1 = ml[pw][0][lane], l1 = ml[pw][1][lane];
+        if constexpr (RES) {
+            // against the true max of both waves: every weight 2^(s·scale − M) <= 1, m in the scores' own units
+            const float M = fmaxf(mt, ml[pw][2][lane]);
+            const float c0 = __builtin_amdgcn_exp2f(m - M), c1 = __builtin_amdgcn_exp2f(m1 - M);
+            if (!row_ok) return;
+            float* rrow = a.res + ((uint64_t)myrow * a.q_heads + head) * (HD + 2);
+            if (par == 0 && half == 0) *(float2*)rrow = make_float2(M * kLn2, l * c0 + l1 * c1);
+#pragma unroll
+            for (int n = 0; n < DT / 2; ++n) {
+                const f32x16 kv = par ? acc[n + DT / 2] : acc[n];
+#pragma unroll
+                for (int qd = 0; qd < 4; ++qd) {
+                    float v4[4];
+#pragma unroll
+                    for (int i = 0; i < 4; ++i)
+                        v4[i] = kv[4 * qd + i] * c0 + X[((pw * (DT / 2) + n) * 16 + 4 * qd + i) * 64 + lane] * c1;
+                    float* at = rrow + 2 + par * (HD / 2) + 32 * n + 8 * qd + 4 * half;
+                    *(float2*)at = make_float2(v4[0], v4[1]);
+                    *(float2*)(at + 2) = make_float2(v4[2], v4[3]);
+                }
+            }
+            return;
+        }
         const float mm = fmaxf(m, m1);
         const float c0 = __builtin_amdgcn_exp2f(m - mm), c1 = __builtin_amdgcn_exp2f(m1 - mm);
         const float inv_l = 1.0f / (l * c0 + l1 * c1);
@@ -1152,7 +1179,7 @@ void causal_paged_launch(uint16_t* o, float* res, const uint16_t* q, const uint1
     // pair row tiles when the causal part dominates the work (a prefix shorter than the chunk)
     const bool paired = first < rows && a.rtiles > 1;
     const dim3 grid(paired ? (a.rtiles + 1) / 2 : a.rtiles, a.kv_heads * a.hblocks);
-    const bool duo = !res && prefill_duo() && a.hw == 4 && head_dim >= 128;
+    const bool duo = prefill_duo() && a.hw == 4 && head_dim >= 128;
     const uint64_t threads = duo ? kDuoThreads : kThreads;
     if ((uint64_t)grid.x * grid.y * threads >= (1ull << 32) || grid.y > 65535) {   // work-items below 2^32
         refuse(what);
@@ -1179,15 +1206,19 @@ void causal_paged_launch(uint16_t* o, float* res, const uint16_t* q, const uint1
     }
     if (duo) {
         const dim3 g2 = grid;
-#define SILVANN_CAUSAL_DUO(HDV) \
+#define SILVANN_CAUSAL_DUO(HDV, R) \
     if (paired) { \
-        if (ptl) causal_duo<HDV, true, true><<<g2, kDuoThreads, 0, st>>>(a); \
-        else causal_duo<HDV, true, false><<<g2, kDuoThreads, 0, st>>>(a); \
+        if (ptl) causal_duo<HDV, true, true, R><<<g2, kDuoThreads, 0, st>>>(a); \
+        else causal_duo<HDV, true, false, R><<<g2, kDuoThreads, 0, st>>>(a); \
     } else { \
-        if (ptl) causal_duo<HDV, false, true><<<g2, kDuoThreads, 0, st>>>(a); \
-        else causal_duo<HDV, false, false><<<g2, kDuoThreads, 0, st>>>(a); \
+        if (ptl) causal_duo<HDV, false, true, R><<<g2, kDuoThreads, 0, st>>>(a); \
+        else causal_duo<HDV, false, false, R><<<g2, kDuoThreads, 0, st>>>(a); \
     }
-        if (head_dim == 128) { SILVANN_CAUSAL_DUO(128) } else { SILVANN_CAUSAL_DUO(256) }
+        if (res) {
+            if (head_dim == 128) { SILVANN_CAUSAL_DUO(128, true) } else { SILVANN_CAUSAL_DUO(256, true) }
+        } else {
+            if (head_dim == 128) { SILVANN_CAUSAL_DUO(128, false) } else { SILVANN_CAUSAL_DUO(256, false) }
+        }
 #undef SILVANN_CAUSAL_DUO
     } else if (res) {
         switch (head_dim) {

@@ -61,6 +61,22 @@ def test_causal_duo_kernel(oracle, hd, qh, kvh, first, rows, ps):
     _causal(oracle, hd, qh, kvh, first, rows, ps, env=DUO)
 
 
+@pytest.mark.parametrize("hd,qh,kvh,first,rows,ps", [
+    (256, 16, 2, 77, 95, 64),    # paged, page table in LDS
+    (128, 4, 1, 1, 33, 0),       # the odd waves' first tile past most rows' positions
+    (256, 8, 2, 300, 40, 32),    # unpaired: a prefix longer than the chunk
+])
+def test_causal_duo_residual_kernel(oracle, hd, qh, kvh, first, rows, ps):
+    """Row 140 through causal_duo (SILVANN_GFX950_PREFILL=duo): the two waves' residuals merged against the true
+    max of both, against the oracle's attention_weights_rows + attention_residual_mix_rows."""
+    w = W.causal("emu", qh, kvh, hd, first, rows, page_size=ps, seed=hd + rows + 5)
+    got, over, _ = emu.run_causal_res(w, DUO)
+    k, v = w.gathered()
+    p, res = oracle.weights_rows(w.q, k, qh, kvh, hd, first, rows)
+    residual_parity(got, oracle.residual_mix_rows(res, p, v, qh, kvh, hd, first, rows), hd)
+    assert over == 0
+
+
 @pytest.mark.parametrize("qh,kvh,hd,lens,ps", [
     (16, 2, 256, [700, 2048], 256),        # paged rows of different lengths
     (8, 2, 128, [1, 17, 300], 0),          # contiguous, a one-position row
