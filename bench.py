@@ -329,7 +329,7 @@ def isolated(n, steps, warmup, limit=240, env=None, variant=None):
     return out
 
 
-def cpu_baseline(w, threads):
+def cpu_baseline(w, threads, budget=20.0):
     """The reference x86_avx2 family over the whole C2 batch (both decode routes, the faster reported); the C
     restatement on one core as "port" where oracle/_ref is absent."""
     import numpy as np
@@ -355,7 +355,6 @@ def cpu_baseline(w, threads):
         routes = {"oracle scores+mix": port}
         kind, cores = "port", 1
     best = None
-    budget = 20.0
     for name, fn in routes.items():
         reps, total, t_all = 0, 0.0, time.perf_counter()
         while True:
