@@ -6,7 +6,8 @@ wave-uniform control flow: its trip count in scalar registers, its back-edge an 
 it writing EXEC. Its bound comes from the wave index (threadIdx.x / 64), which the compiler's divergence analysis
 does not know to be uniform within a wave; left to itself it lowered the loop (and the tail after it) with EXEC
 masks and the tile cursor in vector registers, a form under which an earlier build faulted a GPU. The bound goes
-through readfirstlane for that reason, and this test keeps it so.
+through readfirstlane for that reason, and this test keeps it so. causal_duo's pair loop is held to the same form
+(its tile parity comes from the wave index through readfirstlane); removing that readfirstlane fails the test.
 """
 import os
 import re
@@ -89,3 +90,20 @@ def test_steady_loop_is_wave_uniform(asm):
             assert not bad, f"{name} loop {header} writes EXEC: {bad[:4]}"
             assert not any(re.match(r"\s+s_cbranch_exec", x) and ".LBB" + header[2:] in x for x in body), \
                 f"{name} loop {header} closes on an EXEC branch"
+
+
+def test_duo_pair_loop_is_wave_uniform(asm):
+    """causal_duo's loop over pairs of key tiles (a barrier, the wave's tile's head_dim / 8 MFMAs) branches only on
+    wave-uniform values — the tile parity goes through readfirstlane, the diagonal test and the rescale vote are
+    scalar — so it must not write EXEC either."""
+    ks = {k: v for k, v in kernels(asm).items() if "causal_duoI" in k}
+    assert len(ks) == 16, sorted(ks)   # head_dim 128, 256 x PAIRED x PTL x RES
+    for name, lines in ks.items():
+        mfmas = 32 if "causal_duoILi256E" in name else 16
+        loops = [(h, b) for h, b in outer_loops(lines).items()
+                 if sum("v_mfma" in x for x in b) == mfmas and sum(re.match(r"\s+s_barrier\b", x) is not None
+                                                              for x in b) == 1]
+        assert loops, f"{name}: no pair loop ({mfmas} MFMAs, one barrier) found"
+        for header, body in loops:
+            bad = [x.strip() for x in body if writes_exec(x)]
+            assert not bad, f"{name} loop {header} writes EXEC: {bad[:4]}"
